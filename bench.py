@@ -1,0 +1,220 @@
+"""Benchmark of the gfx950 paged-KV hot path on one MI355X.
+
+Workload: Ouro-1.4B decode over a LAST_EXITED pool —
+64 requests x 4 depth planes, 24 layers, 16 heads x 128, block 16, bf16
+N(0,1)*0.5, context ~ U[512, 4096], each row at a random depth plane. A step
+is one recurrent traversal: for each of the 24 layers, a paged decode call
+over that layer's view of the pool (inputs resident in HBM).
+
+value = algorithmic decode bytes per step / wall time per step, in GB/s
+(K+V of every visible token per row + q/out + page-table entries).
+Also reported (same JSON line): KV-append GB/s for a 24-layer batched append
+of the step's tokens and for the config-4 chunk append (8,240 rows), packed
+prefill TFLOP/s at config 4, the HIP-event roofline of the decode kernel pair,
+and the CPU oracle baseline on a bounded row sample.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _path in (ROOT, os.path.join(ROOT, "vllm-rlt_amd")):
+    if _path not in sys.path:
+        sys.path.insert(0, _path)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse_args():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--skip-extras", action="store_true",
+                        help="only the decode step (no append/prefill/cpu legs)")
+    parser.add_argument("--cpu-seconds", type=float, default=15.0,
+                        help="budget of the CPU baseline sample")
+    return parser.parse_args()
+
+
+def event_time_ms(fn, repeats):
+    """Average HIP-event time of ``fn`` on the current stream."""
+    import torch
+
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+    for i in range(repeats):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / repeats
+
+
+def cpu_baseline(work, budget_s):
+    """Oracle decode (numpy, 1 thread) on a bounded sample of rows of layer 0."""
+    import numpy as np
+    import torch
+
+    from oracle import paged_ref as ref
+
+    rows = work.rows
+    tables = work.block_tables.cpu()
+    lengths = work.context_lengths.cpu()
+    kc, vc = work.key_cache[:, 0], work.value_cache[:, 0]
+    es = kc.element_size()
+    hkv, d = kc.shape[2], kc.shape[3]
+    done_bytes, elapsed, sampled = 0, 0.0, 0
+    for row in range(rows):
+        n = int(lengths[row])
+        pages = tables[row, : -(-n // 16)].to(torch.int64)
+        k_rows = kc[pages.to(kc.device)].float().cpu().numpy()
+        v_rows = vc[pages.to(kc.device)].float().cpu().numpy()
+        local = np.arange(len(pages), dtype=np.int32)[None]
+        q = work.q[row : row + 1].float().cpu().numpy()
+        t0 = time.perf_counter()
+        ref.paged_attention(q, k_rows, v_rows, local, np.array([n], np.int32))
+        elapsed += time.perf_counter() - t0
+        done_bytes += n * 2 * hkv * d * es + 2 * q.size * es + len(pages) * 4
+        sampled += 1
+        if elapsed > budget_s:
+            break
+    return {
+        "value": round(done_bytes / elapsed / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"numpy oracle decode of {sampled}/{rows} config-2 rows of one layer "
+                  f"({elapsed:.1f} s)",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}); this build has no "
+              "multi-GPU path", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from vllm_rlt import workloads
+    from vllm_rlt.kernels._hip import library
+    from vllm_rlt.kernels.hip_attention import (
+        kv_append,
+        kv_append_layers,
+        paged_attention,
+        paged_prefill_attention,
+    )
+
+    library()
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    work = workloads.config2(device=device)
+    layers = work.layers
+    kviews = [work.key_cache[:, layer] for layer in range(layers)]
+    vviews = [work.value_cache[:, layer] for layer in range(layers)]
+    tables, lengths, q = work.block_tables, work.context_lengths, work.q
+
+    def step():
+        for layer in range(layers):
+            paged_attention(q, kviews[layer], vviews[layer], tables, lengths)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    decode_bytes = work.decode_bytes()
+    step_bytes = decode_bytes * layers
+    value = step_bytes / (wall / args.steps) / 1e9
+
+    # HIP-event time of one decode call (split kernel + merge), same stream.
+    call_ms = event_time_ms(lambda: paged_attention(q, kviews[0], vviews[0], tables, lengths),
+                            max(20, args.steps))
+    achieved = decode_bytes / (call_ms * 1e-3) / 1e9
+    result = {
+        "metric": "paged-decode KV GB/s (% of HBM peak) + KV-append GB/s, Ouro-1.4B shape",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "config2: Ouro-1.4B LAST_EXITED decode, 64 rows x 24 layers, "
+                        "16x128 MHA, block 16, ctx U[512,4096], 4 depth planes",
+            "rows": work.rows,
+            "layers": layers,
+            "pool_blocks": work.num_blocks,
+            "decode_bytes_per_layer_call": decode_bytes,
+            "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+            "tokens_per_s": round(work.rows * layers / (wall / args.steps), 1),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "paged_decode_kernel<bf16,8,16> + paged_decode_merge_kernel",
+            "call_ms": round(call_ms, 5),
+        },
+    }
+
+    if not args.skip_extras:
+        # 24-layer batched append of the step's 64 tokens (one launch).
+        append_layers_ms = event_time_ms(
+            lambda: kv_append_layers(work.key_cache, work.value_cache, 0, work.k_new, work.v_new,
+                                     work.write_blocks, work.write_offsets), 50)
+        append_layers_bytes = work.append_bytes(layers)
+        # single-layer decode append (latency)
+        single_ms = event_time_ms(
+            lambda: kv_append(kviews[0], vviews[0], work.k_new[0], work.v_new[0],
+                              work.write_blocks, work.write_offsets), 50)
+        del kviews, vviews
+        extras = {"append_24_layers": {
+            "gbs": round(append_layers_bytes / (append_layers_ms * 1e-3) / 1e9, 2),
+            "us": round(append_layers_ms * 1e3, 2), "bytes": append_layers_bytes},
+            "append_one_layer_us": round(single_ms * 1e3, 2)}
+        result["cpu_baseline"] = cpu_baseline(work, args.cpu_seconds)
+        del work
+        torch.cuda.empty_cache()
+        pw = workloads.config4(device=device)
+        kc, vc = pw.key_cache[:, 0], pw.value_cache[:, 0]
+        append_ms = event_time_ms(
+            lambda: kv_append(kc, vc, pw.k_new, pw.v_new, pw.write_blocks, pw.write_offsets), 50)
+        prefill_ms = event_time_ms(
+            lambda: paged_prefill_attention(pw.q, kc, vc, pw.block_tables, pw.context_lengths,
+                                            pw.cu_seqlens_q, pw.max_seqlen_q), 10)
+        flops = pw.flops()
+        extras["append_config4_chunks"] = {
+            "gbs": round(pw.append_bytes() / (append_ms * 1e-3) / 1e9, 2),
+            "us": round(append_ms * 1e3, 2), "rows": int(pw.k_new.shape[0]),
+            "pct_of_hbm_peak": round(100 * pw.append_bytes() / (append_ms * 1e-3) / 1e9
+                                     / HBM_PEAK_GBS, 2)}
+        extras["prefill_config4"] = {
+            "tflops": round(flops / (prefill_ms * 1e-3) / 1e12, 2), "ms": round(prefill_ms, 4),
+            "pct_of_bf16_mfma_peak": round(100 * flops / (prefill_ms * 1e-3) / 1e12
+                                           / BF16_PEAK_TFLOPS, 2)}
+        result["extras"] = extras
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

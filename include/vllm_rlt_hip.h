@@ -1,0 +1,192 @@
+/*
+ * vllm_rlt_hip.h — C ABI of the MI355X (gfx950) paged KV-cache hot path.
+ *
+ * One shared library (libvllm_rlt_hip.so) exports these entry points. They take
+ * plain device pointers, element strides (int64, in elements of the storage
+ * dtype unless the name says bytes) and a hipStream_t, launch asynchronously on
+ * that stream, never synchronise and never allocate device memory. They return
+ * VRH_OK or an error code; vrh_last_error() then holds a message for the
+ * calling thread.
+ *
+ * Storage layout (the reference's KV pool, kv_cache_manager.py:143-145):
+ *   key_cache, value_cache : [num_blocks, num_layers, block_size, kv_heads, head_dim]
+ * Per-layer entry points receive the layer view K[:, layer], i.e. a base
+ * pointer plus (block, token, head) strides; the head dimension is contiguous.
+ * Block ids are int32 in tables and int64 in write addresses; every physical
+ * offset is computed in 64-bit (pools beyond 2^31 elements).
+ *
+ * Reference interfaces each entry point replaces (paths relative to the
+ * vllm-rlt source tree):
+ *   vrh_kv_append            kv_cache_manager.py:689-699 (index_put append),
+ *                            kernels/routing.py:180-225 (masked_kv_store),
+ *                            kernels/graph_kv.py:7-65 (write_graph_kv)
+ *   vrh_paged_decode         kernels/paged_attention.py:12-71 (torch_paged_attention
+ *                            and its windowed variant), kernels/triton_attention.py:150-202
+ *   vrh_paged_prefill        kernels/triton_attention.py:313-366 (paged_prefill_attention)
+ *   vrh_kv_gather            kv_cache_manager.py:834-854 (read)
+ *   vrh_kv_finalize          kernels/routing.py:147-177 (finalize_kernel),
+ *                            worker/model_runner.py:1331-1346 (its launch)
+ *   vrh_kv_finalize_token    kv_cache_manager.py:806-831 (finalize_token)
+ *   vrh_kv_copy_blocks       kv_cache_manager.py:481-523 (snapshot/restore page
+ *                            copies); also the copy-on-write block copy, which has
+ *                            no counterpart in the reference
+ *   vrh_expand_kv_addresses  kernels/metadata.py:7-24 (expand_kv_addresses)
+ *   vrh_routing_metadata     kernels/routing.py:14-48 (metadata_kernel)
+ *   vrh_routing_slots        kernels/routing.py:7-11 (slots_kernel)
+ */
+#ifndef VLLM_RLT_HIP_H_
+#define VLLM_RLT_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t is an opaque pointer; 0 selects the null stream. */
+typedef struct ihipStream_t* vrh_stream_t;
+
+enum {
+  VRH_OK = 0,
+  VRH_ERROR_INVALID_ARG = 1,
+  VRH_ERROR_LAUNCH = 2,
+  VRH_ERROR_UNSUPPORTED = 3,
+};
+
+enum {
+  VRH_DTYPE_F32 = 0,
+  VRH_DTYPE_F16 = 1,
+  VRH_DTYPE_BF16 = 2,
+};
+
+/* ABI version of this header; bumped on any signature change. */
+int vrh_abi_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char* vrh_last_error(void);
+
+/* ------------------------------------------------------------------ append
+ * For every row r < rows that is enabled, and every layer l < layers:
+ *   cache[write_blocks[r], l, write_offsets[r], h, d] = k[l, r, h, d]   (same for v)
+ * A row is enabled when (active_rows == NULL || r < *active_rows) and
+ * (write_mask == NULL || write_mask[r] != 0). Disabled rows are not touched.
+ * `layers` > 1 batches the appends of several layers (k/v layer strides and
+ * the cache layer stride select them); pass layers = 1 for one layer view.
+ * Bit-exact copy. */
+int vrh_kv_append(int dtype, void* key_cache, void* value_cache, int64_t cache_block_stride,
+                  int64_t cache_token_stride, int64_t cache_head_stride,
+                  int64_t cache_layer_stride, const void* k, const void* v, int64_t k_row_stride,
+                  int64_t k_head_stride, int64_t k_layer_stride, int64_t v_row_stride,
+                  int64_t v_head_stride, int64_t v_layer_stride, const int64_t* write_blocks,
+                  const int64_t* write_offsets, const uint8_t* write_mask,
+                  const int32_t* active_rows, int64_t rows, int32_t layers, int32_t kv_heads,
+                  int32_t head_dim, vrh_stream_t stream);
+
+/* ------------------------------------------------------------ paged decode
+ * Single-query attention per row over its own block table:
+ *   out[r, h] = softmax(q[r, h] . K[t, h / G]^T / sqrt(D)) V[t, h / G],  t in window
+ * where G = q_heads / kv_heads, t ranges over [max(0, n - window), n) with
+ * n = context_lengths[r] (window = 0: the whole context), K[t] is
+ * key_cache[block_tables[r, t / block_size], t % block_size]. Rows with n = 0
+ * produce zeros. fp32 accumulation; the output is rounded to the storage dtype.
+ * The result of a row depends only on that row's inputs (batch invariant).
+ * `workspace` must hold vrh_paged_decode_workspace_bytes(rows, q_heads, head_dim)
+ * bytes of device memory; it needs no initialisation. */
+size_t vrh_paged_decode_workspace_bytes(int64_t rows, int32_t q_heads, int32_t head_dim);
+int vrh_paged_decode(int dtype, void* out, const void* q, const void* key_cache,
+                     const void* value_cache, const int32_t* block_tables,
+                     const int32_t* context_lengths, int64_t rows, int32_t q_heads,
+                     int32_t kv_heads, int32_t head_dim, int32_t block_size, int32_t table_width,
+                     int64_t table_stride, int64_t q_row_stride, int64_t q_head_stride,
+                     int64_t out_row_stride, int64_t out_head_stride, int64_t k_block_stride,
+                     int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
+                     int64_t v_token_stride, int64_t v_head_stride, int32_t window,
+                     void* workspace, size_t workspace_bytes, vrh_stream_t stream);
+
+/* ----------------------------------------------------------- paged prefill
+ * Packed causal prefill, bottom-right aligned: sequence s owns query rows
+ * [cu_seqlens_q[s], cu_seqlens_q[s+1]) and keys [0, context_lengths[s]) through
+ * block_tables[s]; its query i sits at position n_s - q_s + i and attends keys
+ * at positions <= that. bf16/f16 use MFMA with fp32 accumulation; f32 uses
+ * fp32 MFMA (exact products). */
+int vrh_paged_prefill(int dtype, void* out, const void* q, const void* key_cache,
+                      const void* value_cache, const int32_t* block_tables,
+                      const int32_t* context_lengths, const int32_t* cu_seqlens_q,
+                      int64_t num_seqs, int64_t total_q, int32_t max_seqlen_q, int32_t q_heads,
+                      int32_t kv_heads, int32_t head_dim, int32_t block_size,
+                      int32_t table_width, int64_t table_stride, int64_t q_token_stride,
+                      int64_t q_head_stride, int64_t out_token_stride, int64_t out_head_stride,
+                      int64_t k_block_stride, int64_t k_token_stride, int64_t k_head_stride,
+                      int64_t v_block_stride, int64_t v_token_stride, int64_t v_head_stride,
+                      vrh_stream_t stream);
+
+/* ------------------------------------------------------------------ gather
+ * out_k[t] = K[table[t / block_size], t % block_size] for t < length (and V),
+ * where K is a layer view; out rows are `channel_bytes` contiguous bytes
+ * (kv_heads * head_dim * elem_size). Bit-exact. */
+int vrh_kv_gather(void* out_k, void* out_v, const void* key_cache, const void* value_cache,
+                  const int32_t* table, int64_t length, int32_t block_size,
+                  int64_t block_stride_bytes, int64_t token_stride_bytes, int64_t channel_bytes,
+                  vrh_stream_t stream);
+
+/* ---------------------------------------------------------------- finalize
+ * LAST_EXITED depth propagation from device descriptors. For each row r with
+ * (slot, depth, pos) = descriptors[r, 0:3] and each plane p in (depth, planes):
+ *   src = tables[(slot * planes + depth) * width + pos / block_size]
+ *   dst = tables[(slot * planes + p) * width + pos / block_size]
+ *   K[dst, l, pos % block_size, :] = K[src, l, pos % block_size, :]  for all l < layers
+ * (same for V). Strides are in bytes; a (layer, token) slot is channel_bytes
+ * contiguous bytes. Bit-exact. */
+int vrh_kv_finalize(void* key_cache, void* value_cache, const int64_t* descriptors,
+                    const int32_t* tables, int64_t rows, int32_t planes, int32_t width,
+                    int32_t block_size, int32_t layers, int64_t block_stride_bytes,
+                    int64_t layer_stride_bytes, int64_t token_stride_bytes,
+                    int64_t channel_bytes, vrh_stream_t stream);
+
+/* Host-described variant for one token: copies the slot `offset` of the
+ * listed layers from block `src_block` into each of `dst_blocks[0:num_dst]`
+ * (host arrays, num_dst <= 64, num_layers <= 256). */
+int vrh_kv_finalize_token(void* key_cache, void* value_cache, int64_t src_block,
+                          const int64_t* dst_blocks, int32_t num_dst, int32_t offset,
+                          const int32_t* layer_ids, int32_t num_layers,
+                          int64_t block_stride_bytes, int64_t layer_stride_bytes,
+                          int64_t token_stride_bytes, int64_t channel_bytes,
+                          vrh_stream_t stream);
+
+/* -------------------------------------------------------------- block copy
+ * For i < n: bytes [0, block_bytes) of block dst_blocks[i] = those of block
+ * src_blocks[i], in both caches. Block ids index `block_stride_bytes`-strided
+ * blocks of the whole pool (all layers). Source and destination sets must be
+ * disjoint. Bit-exact. */
+int vrh_kv_copy_blocks(void* key_cache, void* value_cache, int64_t block_stride_bytes,
+                       int64_t block_bytes, const int64_t* src_blocks, const int64_t* dst_blocks,
+                       int64_t n, vrh_stream_t stream);
+
+/* --------------------------------------------------------------- addresses
+ * blocks[i] = tables[sequences[i] * width + positions[i] / page],
+ * offsets[i] = positions[i] % page, for i < n. */
+int vrh_expand_kv_addresses(const int64_t* positions, const int32_t* sequences,
+                            const int32_t* tables, int64_t* blocks, int64_t* offsets, int64_t n,
+                            int32_t width, int32_t page, vrh_stream_t stream);
+
+/* Per row r < size (valid when r < n), from descriptors[r] = (slot, depth, pos):
+ *   plane = planes > 1 ? depth : 0; base = (slot * planes + plane) * width
+ *   slots[r] = slot, positions[r] = pos, lengths[r] = valid ? pos + 1 : 0
+ *   blocks[r] = tables[base + pos / page], offsets[r] = pos % page  (valid rows only)
+ *   out_tables[r * width + c] = valid ? tables[base + c] : 0  for c < out_width
+ * Invalid rows read slot = depth = pos = 0. */
+int vrh_routing_metadata(const int64_t* descriptors, const int32_t* tables, int64_t* slots,
+                         int64_t* positions, int32_t* lengths, int64_t* blocks,
+                         int64_t* offsets, int32_t* out_tables, int64_t n, int64_t size,
+                         int32_t width, int32_t page, int32_t planes, int32_t out_width,
+                         vrh_stream_t stream);
+
+/* slots[r] = r < n ? descriptors[r * 3] : 0 for r < size. */
+int vrh_routing_slots(const int64_t* descriptors, int64_t* slots, int64_t n, int64_t size,
+                      vrh_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VLLM_RLT_HIP_H_ */

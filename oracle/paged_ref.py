@@ -1,0 +1,215 @@
+"""CPU oracle of the paged KV hot path — TEST INFRASTRUCTURE ONLY.
+
+A numpy restatement of the reference's Torch path. Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import this module, and only as the checker / baseline; the product path
+(``vllm-rlt_amd/vllm_rlt``) never calls it.
+
+Arrays: float storage is passed as float32 arrays (bf16/f16 inputs are widened
+exactly beforehand with :func:`bf16_bits_to_f32` / ``astype``); integer
+metadata as int32/int64 arrays. Caches are per-layer views
+``[num_blocks, block_size, kv_heads, head_dim]`` or whole pools
+``[num_blocks, layers, block_size, kv_heads, head_dim]``.
+
+Pinning (tests/test_oracle.py): attention against torch's
+``scaled_dot_product_attention`` (an independent library routine), closed forms
+(length 0 -> zeros, length 1 -> V row, constant keys -> mean of V, the
+closed-form early-exit means of the reference's tests), window = slicing, the
+literal integer vectors of the reference's metadata tests, and brute-force
+loops for the integer kernels.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+# ------------------------------------------------------------ bf16 helpers
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    """Exact widening of raw bf16 bit patterns (uint16/int16) to float32."""
+    return (bits.astype(np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round float32 to bf16 bit patterns, nearest-even (NaN stays NaN)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    if nan.any():
+        rounded = np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), rounded)
+    return rounded
+
+
+def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Round float32 values to ``dtype`` ('f32', 'f16', 'bf16') and widen back."""
+    if dtype == "f32":
+        return x.astype(np.float32)
+    if dtype == "f16":
+        return x.astype(np.float16).astype(np.float32)
+    if dtype == "bf16":
+        return bf16_bits_to_f32(f32_to_bf16_bits(x))
+    raise ValueError(dtype)
+
+
+# -------------------------------------------------------------- attention
+def paged_attention(q, key_cache, value_cache, block_tables, context_lengths, window=0):
+    """Per-row gather -> fp32 scores -> softmax -> weighted V.
+
+    Follows kernels/paged_attention.py:12-36 (window = 0) and :39-71
+    (window > 0: the last ``window`` keys). GQA: q head h reads kv head
+    h // (Hq / Hkv) (the repeat_interleave of :31-32). Length-0 rows are zero.
+    Returns float32 ``[rows, Hq, D]`` (round with :func:`round_to`).
+    """
+    q = np.asarray(q, dtype=np.float32)
+    rows, heads, dim = q.shape
+    block_size = key_cache.shape[1]
+    groups = heads // key_cache.shape[2]
+    scale = np.float32(1.0 / math.sqrt(dim))
+    out = np.zeros((rows, heads, dim), dtype=np.float32)
+    for row in range(rows):
+        length = int(context_lengths[row])
+        if length == 0:
+            continue
+        start = max(0, length - window) if window else 0
+        positions = np.arange(start, length)
+        blocks = np.asarray(block_tables[row])[positions // block_size]
+        offsets = positions % block_size
+        keys = np.repeat(key_cache[blocks, offsets].astype(np.float32), groups, axis=1)
+        values = np.repeat(value_cache[blocks, offsets].astype(np.float32), groups, axis=1)
+        scores = np.einsum("hd,thd->ht", q[row], keys).astype(np.float32) * scale
+        scores = scores - scores.max(axis=-1, keepdims=True)
+        weights = np.exp(scores)
+        weights /= weights.sum(axis=-1, keepdims=True)
+        out[row] = np.einsum("ht,thd->hd", weights, values)
+    return out
+
+
+def prefill_rows(block_tables, context_lengths, cu_seqlens_q):
+    """Expand packed sequences into per-query decode rows (table row, length).
+
+    Query i of sequence s sits at position n_s - q_s + i and sees keys
+    0 .. that position (triton_attention.py:241-263,281; the per-row expansion
+    of tests/test_attention.py:333-346)."""
+    tables, lengths = [], []
+    for s in range(len(context_lengths)):
+        q_len = int(cu_seqlens_q[s + 1]) - int(cu_seqlens_q[s])
+        n = int(context_lengths[s])
+        for i in range(q_len):
+            tables.append(np.asarray(block_tables[s]))
+            lengths.append(max(0, n - q_len + i + 1))
+    if not tables:
+        return np.zeros((0, 0), np.int32), np.zeros(0, np.int32)
+    return np.stack(tables), np.asarray(lengths, np.int32)
+
+
+def paged_prefill(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q):
+    """Packed causal prefill, bottom-right aligned (triton_attention.py:313-366)."""
+    tables, lengths = prefill_rows(block_tables, context_lengths, cu_seqlens_q)
+    return paged_attention(q, key_cache, value_cache, tables, lengths)
+
+
+# ------------------------------------------------------------- KV writes
+def kv_append(key_cache, value_cache, k, v, write_blocks, write_offsets, write_mask=None,
+              active_rows=None):
+    """In place: ``cache[block_r, offset_r] = k[r]`` for enabled rows.
+
+    Follows kv_cache_manager.py:698-699 (index_put), routing.py:193-205
+    (write_mask) and graph_kv.py:23-46 (rows < active_rows)."""
+    for r in range(len(write_blocks)):
+        if active_rows is not None and r >= int(active_rows):
+            continue
+        if write_mask is not None and not bool(write_mask[r]):
+            continue
+        key_cache[int(write_blocks[r]), int(write_offsets[r])] = k[r]
+        value_cache[int(write_blocks[r]), int(write_offsets[r])] = v[r]
+
+
+def kv_gather(key_cache, value_cache, table, length):
+    """``K[table[t // bs], t % bs]`` for t < length (kv_cache_manager.py:848-854)."""
+    positions = np.arange(length)
+    blocks = np.asarray(table, dtype=np.int64)[positions // key_cache.shape[1]]
+    offsets = positions % key_cache.shape[1]
+    return key_cache[blocks, offsets].copy(), value_cache[blocks, offsets].copy()
+
+
+def finalize_rows(key_pool, value_pool, descriptors, tables, planes):
+    """In place, for pools ``[N, L, bs, H, D]``: each row (slot, depth, pos)
+    copies its exit plane's token slot (every layer) into planes > depth
+    (routing.py:147-177)."""
+    width = tables.shape[1]
+    bs = key_pool.shape[2]
+    flat = np.asarray(tables).reshape(-1)
+    for slot, depth, pos in np.asarray(descriptors, dtype=np.int64):
+        for target in range(planes):
+            if target <= depth:
+                continue
+            src = flat[(slot * planes + depth) * width + pos // bs]
+            dst = flat[(slot * planes + target) * width + pos // bs]
+            key_pool[dst, :, pos % bs] = key_pool[src, :, pos % bs]
+            value_pool[dst, :, pos % bs] = value_pool[src, :, pos % bs]
+
+
+def finalize_token(key_pool, value_pool, source, destinations, offset, layers):
+    """In place: copy slot ``offset`` of ``layers`` from block ``source`` into each
+    destination block (kv_cache_manager.py:815-830)."""
+    for dst in destinations:
+        for layer in layers:
+            key_pool[dst, layer, offset] = key_pool[source, layer, offset]
+            value_pool[dst, layer, offset] = value_pool[source, layer, offset]
+
+
+def copy_blocks(key_pool, value_pool, src, dst):
+    """In place: whole-block copies ``pool[dst[i]] = pool[src[i]]``."""
+    for s, d in zip(src, dst):
+        key_pool[int(d)] = key_pool[int(s)]
+        value_pool[int(d)] = value_pool[int(s)]
+
+
+# --------------------------------------------------------------- addresses
+def expand_kv_addresses(positions, sequences, tables, page):
+    """(blocks, offsets) of packed query rows (kernels/metadata.py:7-24)."""
+    positions = np.asarray(positions, dtype=np.int64)
+    sequences = np.asarray(sequences, dtype=np.int64)
+    blocks = np.asarray(tables, dtype=np.int64)[sequences, positions // page]
+    return blocks, positions % page
+
+
+def routing_metadata(descriptors, tables, n, size, width, page, planes, out_width):
+    """Outputs of ``metadata_kernel`` (routing.py:14-48) for rows < size.
+
+    Returns dict with slots, positions (int64), lengths (int32), blocks,
+    offsets (int64; only rows < n defined, others left at -1), out_tables
+    (int32 ``[size, width]`` with columns >= out_width left at -1)."""
+    flat = np.asarray(tables, dtype=np.int64).reshape(-1)
+    result = {
+        "slots": np.zeros(size, np.int64),
+        "positions": np.zeros(size, np.int64),
+        "lengths": np.zeros(size, np.int32),
+        "blocks": np.full(size, -1, np.int64),
+        "offsets": np.full(size, -1, np.int64),
+        "out_tables": np.full((size, width), -1, np.int32),
+    }
+    for row in range(size):
+        valid = row < n
+        slot, depth, pos = (np.asarray(descriptors[row], np.int64) if valid else (0, 0, 0))
+        plane = depth if planes > 1 else 0
+        base = (slot * planes + plane) * width
+        result["slots"][row] = slot
+        result["positions"][row] = pos
+        result["lengths"][row] = pos + 1 if valid else 0
+        if valid:
+            result["blocks"][row] = flat[base + pos // page]
+            result["offsets"][row] = pos % page
+        for col in range(out_width):
+            result["out_tables"][row, col] = flat[base + col] if valid else 0
+    return result
+
+
+def routing_slots(descriptors, n, size):
+    """``slots_kernel`` (routing.py:7-11)."""
+    out = np.zeros(size, np.int64)
+    for row in range(min(n, size)):
+        out[row] = descriptors[row][0]
+    return out

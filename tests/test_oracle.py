@@ -1,0 +1,213 @@
+"""Pins the CPU oracle itself (CPU only).
+
+Each check can fail for a plausible mistake in the oracle (wrong scale, GQA
+head mapping, off-by-one window or causal length, dropped rows):
+  * attention == torch.nn.functional.scaled_dot_product_attention (independent
+    library routine; the reference pins its Torch path the same way,
+    tests/test_attention.py:8-15,203-255);
+  * closed forms: length 0 -> zeros, length 1 -> V row, constant keys -> mean V,
+    window == slicing the history, the closed-form early-exit means of
+    tests/test_kv_cache.py:61-77;
+  * the committed golden fixture (tests/golden/decode_small.npz);
+  * integer kernels against brute-force loops / literal vectors.
+"""
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+from torch.nn import functional as F
+
+from oracle import paged_ref as ref
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def sdpa_rows(q, keys_per_row, values_per_row, groups):
+    out = []
+    for row in range(q.shape[0]):
+        k = torch.from_numpy(keys_per_row[row]).repeat_interleave(groups, dim=1)
+        v = torch.from_numpy(values_per_row[row]).repeat_interleave(groups, dim=1)
+        if k.shape[0] == 0:
+            out.append(torch.zeros(q.shape[1], q.shape[2]))
+            continue
+        o = F.scaled_dot_product_attention(
+            torch.from_numpy(q[row])[:, None], k.transpose(0, 1), v.transpose(0, 1)
+        )
+        out.append(o[:, 0])
+    return torch.stack(out).numpy()
+
+
+def random_case(rng, lengths, heads=4, kv_heads=2, dim=16, block=4):
+    pages = sum(-(-n // block) for n in lengths) + 2
+    kc = rng.standard_normal((pages, block, kv_heads, dim)).astype(np.float32)
+    vc = rng.standard_normal((pages, block, kv_heads, dim)).astype(np.float32)
+    order = list(rng.permutation(pages))
+    width = max(1, max(-(-n // block) for n in lengths))
+    tables = np.full((len(lengths), width), -1, np.int32)
+    for row, n in enumerate(lengths):
+        for p in range(-(-n // block)):
+            tables[row, p] = order.pop()
+    q = rng.standard_normal((len(lengths), heads, dim)).astype(np.float32)
+    return q, kc, vc, tables, np.asarray(lengths, np.int32)
+
+
+def history(kc, tables, lengths, start=None):
+    block = kc.shape[1]
+    out = []
+    for row, n in enumerate(lengths):
+        s = 0 if start is None else start[row]
+        pos = np.arange(s, n)
+        out.append(kc[tables[row][pos // block], pos % block])
+    return out
+
+
+def test_attention_matches_sdpa_with_gqa():
+    rng = np.random.default_rng(0)
+    q, kc, vc, tables, lengths = random_case(rng, [0, 1, 3, 4, 5, 17, 40])
+    actual = ref.paged_attention(q, kc, vc, tables, lengths)
+    expected = sdpa_rows(q, history(kc, tables, lengths), history(vc, tables, lengths), 2)
+    np.testing.assert_allclose(actual, expected, atol=2e-6, rtol=2e-5)
+
+
+def test_window_equals_sliced_history():
+    rng = np.random.default_rng(1)
+    q, kc, vc, tables, lengths = random_case(rng, [0, 1, 6, 9, 30])
+    for window in (1, 2, 7, 100):
+        start = [max(0, n - window) for n in lengths]
+        actual = ref.paged_attention(q, kc, vc, tables, lengths, window=window)
+        expected = sdpa_rows(q, history(kc, tables, lengths, start),
+                             history(vc, tables, lengths, start), 2)
+        np.testing.assert_allclose(actual, expected, atol=2e-6, rtol=2e-5)
+
+
+def test_closed_forms():
+    rng = np.random.default_rng(2)
+    q, kc, vc, tables, _ = random_case(rng, [8, 8])
+    lengths = np.array([1, 0], np.int32)
+    out = ref.paged_attention(q, kc, vc, tables, lengths)
+    np.testing.assert_array_equal(out[0], np.repeat(vc[tables[0, 0], 0], 2, axis=0))
+    assert not out[1].any()
+    kc[:] = 0.75  # constant keys: uniform weights
+    lengths = np.array([7, 8], np.int32)
+    out = ref.paged_attention(q, kc, vc, tables, lengths)
+    for row in range(2):
+        mean = history(vc, tables, lengths)[row].mean(axis=0)
+        np.testing.assert_allclose(out[row], np.repeat(mean, 2, axis=0), atol=1e-6)
+
+
+def test_early_exit_closed_form_means():
+    """tests/test_kv_cache.py:61-77 restated: value at (p, d, layer) is
+    100 + 10p + min(p, d) + layer with zero queries -> plain mean."""
+    layer, block = 1, 2
+    for position, depth in [(0, 0), (1, 1), (2, 2), (2, 1)]:
+        n = position + 1
+        vc = np.zeros((2, block, 1, 4), np.float32)
+        for p in range(n):
+            vc[p // block, p % block] = 100 + 10 * p + min(p, depth) + layer
+        kc = np.ones_like(vc)
+        tables = np.array([[0, 1]], np.int32)
+        out = ref.paged_attention(np.zeros((1, 2, 4), np.float32), kc, vc, tables,
+                                  np.array([n], np.int32))
+        expected = np.mean([100 + 10 * p + min(p, depth) + layer for p in range(n)])
+        np.testing.assert_allclose(out, np.full_like(out, expected), rtol=1e-6)
+
+
+def test_prefill_rows_are_bottom_right_aligned():
+    tables, lengths = ref.prefill_rows(np.array([[1, 2], [3, 4]], np.int32),
+                                       np.array([5, 3], np.int32), np.array([0, 2, 5]))
+    assert lengths.tolist() == [4, 5, 1, 2, 3]
+    assert tables[:, 0].tolist() == [1, 1, 3, 3, 3]
+
+
+def test_prefill_matches_causal_sdpa():
+    rng = np.random.default_rng(3)
+    dim, block, heads = 8, 4, 2
+    n, q_len = 11, 5
+    kc = rng.standard_normal((4, block, heads, dim)).astype(np.float32)
+    vc = rng.standard_normal((4, block, heads, dim)).astype(np.float32)
+    tables = np.array([[2, 0, 3]], np.int32)
+    q = rng.standard_normal((q_len, heads, dim)).astype(np.float32)
+    out = ref.paged_prefill(q, kc, vc, tables, np.array([n], np.int32), np.array([0, q_len]))
+    keys = torch.from_numpy(history(kc, tables, [n])[0]).transpose(0, 1)
+    values = torch.from_numpy(history(vc, tables, [n])[0]).transpose(0, 1)
+    mask = torch.arange(n)[None, :] <= (n - q_len + torch.arange(q_len))[:, None]
+    expected = F.scaled_dot_product_attention(torch.from_numpy(q).transpose(0, 1), keys, values,
+                                              attn_mask=mask)
+    np.testing.assert_allclose(out, expected.transpose(0, 1).numpy(), atol=2e-6, rtol=2e-5)
+
+
+def test_bf16_rounding_matches_torch():
+    x = np.random.default_rng(4).standard_normal(10000).astype(np.float32) * 100
+    x[:4] = [np.inf, -np.inf, 0.0, -0.0]
+    ours = ref.f32_to_bf16_bits(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().astype(np.uint16)
+    assert np.array_equal(ours, theirs)
+    np.testing.assert_array_equal(ref.bf16_bits_to_f32(ours),
+                                  torch.from_numpy(x).to(torch.bfloat16).float().numpy())
+
+
+def test_golden_fixture_reproduces():
+    data = np.load(os.path.join(GOLDEN, "decode_small.npz"))
+    out = ref.paged_attention(data["q"], data["k"], data["v"], data["tables"], data["lengths"])
+    np.testing.assert_allclose(out, data["out"], atol=1e-6, rtol=1e-6)
+    groups = data["q"].shape[1] // data["k"].shape[2]
+    expected = sdpa_rows(data["q"], history(data["k"], data["tables"], data["lengths"]),
+                         history(data["v"], data["tables"], data["lengths"]), groups)
+    np.testing.assert_allclose(data["out"], expected, atol=2e-6, rtol=2e-5)
+
+
+def test_integer_kernels_brute_force():
+    rng = np.random.default_rng(5)
+    tables = rng.integers(0, 1000, (5, 6)).astype(np.int32)
+    positions = rng.integers(0, 96, 40)
+    sequences = rng.integers(0, 5, 40)
+    blocks, offsets = ref.expand_kv_addresses(positions, sequences, tables, 16)
+    for i in range(40):
+        assert blocks[i] == tables[sequences[i]][positions[i] // 16]
+        assert offsets[i] == positions[i] - 16 * (positions[i] // 16)
+    # metadata_kernel literal case: slot 1, depth 2, pos 17 of a 3-plane table.
+    route = np.arange(2 * 3 * 4, dtype=np.int32).reshape(6, 4) + 100
+    out = ref.routing_metadata(np.array([[1, 2, 17]]), route, n=1, size=2, width=4, page=16,
+                               planes=3, out_width=3)
+    assert out["blocks"].tolist()[0] == 100 + (1 * 3 + 2) * 4 + 1
+    assert out["lengths"].tolist() == [18, 0]
+    assert out["out_tables"].tolist() == [[120, 121, 122, -1], [0, 0, 0, -1]]
+    assert ref.routing_slots(np.array([[7, 0, 0], [3, 1, 1]]), 2, 3).tolist() == [7, 3, 0]
+
+
+def test_kv_movement_closed_forms():
+    pool_k = np.arange(4 * 2 * 2 * 1 * 3, dtype=np.float32).reshape(4, 2, 2, 1, 3)
+    pool_v = -pool_k
+    tables = np.array([[0, 1], [2, 3]], np.int32)  # slot 0: plane 0 = [0, 1], plane 1 = [2, 3]
+    k2, v2 = pool_k.copy(), pool_v.copy()
+    ref.finalize_rows(k2, v2, np.array([[0, 0, 3]]), tables, planes=2)
+    np.testing.assert_array_equal(k2[3, :, 1], pool_k[1, :, 1])
+    changed = (k2 != pool_k)
+    assert changed[3, :, 1].all() and changed.sum() == changed[3, :, 1].size
+    k3, v3 = pool_k.copy(), pool_v.copy()
+    ref.copy_blocks(k3, v3, [0], [2])
+    np.testing.assert_array_equal(k3[2], pool_k[0])
+    np.testing.assert_array_equal(v3[2], pool_v[0])
+    keys, values = ref.kv_gather(pool_k[:, 1], pool_v[:, 1], [3, 0], 3)
+    np.testing.assert_array_equal(keys, np.stack([pool_k[3, 1, 0], pool_k[3, 1, 1],
+                                                  pool_k[0, 1, 0]]))
+    kc = np.zeros((3, 2, 1, 2), np.float32)
+    vc = np.zeros_like(kc)
+    k = np.arange(6, dtype=np.float32).reshape(3, 1, 2)
+    ref.kv_append(kc, vc, k, -k, [2, 0, 1], [1, 0, 1], write_mask=[1, 1, 0], active_rows=2)
+    np.testing.assert_array_equal(kc[2, 1], k[0])
+    np.testing.assert_array_equal(kc[0, 0], k[1])
+    assert not kc[1].any()
+    assert math.isclose(float(vc[2, 1, 0, 1]), -1.0)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_oracle_handles_fp16_widening(seed):
+    rng = np.random.default_rng(seed)
+    q, kc, vc, tables, lengths = random_case(rng, [5, 9])
+    half = [x.astype(np.float16).astype(np.float32) for x in (q, kc, vc)]
+    out = ref.paged_attention(*half, tables, lengths)
+    assert out.dtype == np.float32 and np.isfinite(out).all()

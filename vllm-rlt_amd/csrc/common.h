@@ -1,0 +1,202 @@
+// Shared device helpers for the gfx950 paged-KV kernels.
+//
+// Storage types: float (f32), _Float16 (f16) and bf16 kept as raw uint16_t bits.
+// Every kernel computes in fp32 and converts on load/store; bf16 stores round to
+// nearest even, which is what torch's `.to(torch.bfloat16)` does.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vllm_rlt_hip.h"
+
+namespace vrh {
+
+struct bf16_t {
+  uint16_t bits;
+};
+using f16_t = _Float16;
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(f16_t x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16_t x) {
+  return __uint_as_float(((uint32_t)x.bits) << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ f16_t from_f32<f16_t>(float x) { return (f16_t)x; }
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
+  uint32_t u = __float_as_uint(x);
+  bf16_t r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {  // NaN: keep it quiet, keep the sign
+    r.bits = (uint16_t)((u >> 16) | 0x0040u);
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest, ties to even
+    r.bits = (uint16_t)(u >> 16);
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------- raw vectors
+// A VEC-element vector of T loaded/stored as one global instruction
+// (16 B = global_load_dwordx4 when VEC * sizeof(T) == 16).
+template <int BYTES>
+struct RawVec;
+template <>
+struct RawVec<1> {
+  using type = uint8_t;
+};
+template <>
+struct RawVec<2> {
+  using type = uint16_t;
+};
+template <>
+struct RawVec<4> {
+  using type = uint32_t;
+};
+template <>
+struct RawVec<8> {
+  using type = __attribute__((ext_vector_type(2))) uint32_t;
+};
+template <>
+struct RawVec<16> {
+  using type = __attribute__((ext_vector_type(4))) uint32_t;
+};
+
+template <typename T, int VEC>
+struct Vec {
+  static constexpr int kBytes = VEC * (int)sizeof(T);
+  using raw_t = typename RawVec<kBytes>::type;
+  union {
+    raw_t raw;
+    T e[VEC];
+  };
+};
+
+template <typename T, int VEC>
+__device__ __forceinline__ typename Vec<T, VEC>::raw_t load_raw(const T* p) {
+  return *reinterpret_cast<const typename Vec<T, VEC>::raw_t*>(p);
+}
+
+// Non-temporal variant for streams that are read exactly once (K/V tiles).
+template <typename T, int VEC>
+__device__ __forceinline__ typename Vec<T, VEC>::raw_t load_raw_stream(const T* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const typename Vec<T, VEC>::raw_t*>(p));
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void store_raw(T* p, typename Vec<T, VEC>::raw_t v) {
+  *reinterpret_cast<typename Vec<T, VEC>::raw_t*>(p) = v;
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void unpack(typename Vec<T, VEC>::raw_t raw, float (&out)[VEC]) {
+  Vec<T, VEC> v;
+  v.raw = raw;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) out[i] = to_f32(v.e[i]);
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ typename Vec<T, VEC>::raw_t pack(const float (&in)[VEC]) {
+  Vec<T, VEC> v;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) v.e[i] = from_f32<T>(in[i]);
+  return v.raw;
+}
+
+// ------------------------------------------------------------ wave reductions
+// DPP control words (GCN/CDNA "row" = 16 lanes).
+constexpr int kDppQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <-> 7-i within 8
+constexpr int kDppRowMirror = 0x140;      // lane i <-> 15-i within 16
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float shfl_xor_f32(float x, int mask) {
+  int lane = __lane_id();
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(x)));
+}
+
+__device__ __forceinline__ int shfl_i32(int x, int src_lane) {
+  return __builtin_amdgcn_ds_bpermute(src_lane << 2, x);
+}
+
+// Sum over aligned groups of WIDTH lanes (WIDTH a power of two <= 64); every
+// lane of the group receives the group total.
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (WIDTH >= 2) x += dpp_f32<kDppQuadXor1>(x);
+  if constexpr (WIDTH >= 4) x += dpp_f32<kDppQuadXor2>(x);
+  if constexpr (WIDTH >= 8) x += dpp_f32<kDppRowHalfMirror>(x);
+  if constexpr (WIDTH >= 16) x += dpp_f32<kDppRowMirror>(x);
+  if constexpr (WIDTH >= 32) x += shfl_xor_f32(x, 16);
+  if constexpr (WIDTH >= 64) x += shfl_xor_f32(x, 32);
+  return x;
+}
+
+// Reductions across the lane groups that differ in bits [LOG_FROM, 6) of the
+// lane id (i.e. across token groups when each group spans 1 << LOG_FROM lanes).
+template <int FROM>
+__device__ __forceinline__ float cross_group_max(float x) {
+#pragma unroll
+  for (int m = FROM; m < 64; m <<= 1) x = fmaxf(x, shfl_xor_f32(x, m));
+  return x;
+}
+template <int FROM>
+__device__ __forceinline__ float cross_group_sum(float x) {
+#pragma unroll
+  for (int m = FROM; m < 64; m <<= 1) x += shfl_xor_f32(x, m);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, shfl_xor_f32(x, m));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) x += shfl_xor_f32(x, m);
+  return x;
+}
+
+__host__ __device__ __forceinline__ int64_t ceil_div64(int64_t a, int64_t b) {
+  return (a + b - 1) / b;
+}
+__host__ __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace vrh
+
+// --------------------------------------------------------------- host helpers
+// Last error text, per thread; set by every entry point that fails.
+void vrh_set_error(const char* fmt, ...);
+
+#define VRH_CHECK_ARG(cond, ...)     \
+  do {                               \
+    if (!(cond)) {                   \
+      vrh_set_error(__VA_ARGS__);    \
+      return VRH_ERROR_INVALID_ARG;  \
+    }                                \
+  } while (0)
+
+#define VRH_RETURN_LAUNCH(what)                                                         \
+  do {                                                                                  \
+    hipError_t _e = hipGetLastError();                                                  \
+    if (_e != hipSuccess) {                                                             \
+      vrh_set_error("%s: kernel launch failed: %s", what, hipGetErrorString(_e));       \
+      return VRH_ERROR_LAUNCH;                                                          \
+    }                                                                                   \
+    return VRH_OK;                                                                      \
+  } while (0)

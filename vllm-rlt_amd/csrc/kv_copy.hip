@@ -1,0 +1,323 @@
+// Bit-exact KV movement kernels: whole-block copy (preemption snapshot/restore
+// staging and copy-on-write), LAST_EXITED depth propagation (finalize) and the
+// block-table gather that materialises a request's history (read).
+//
+// All of them are byte copies, so they are written once over raw bytes with the
+// widest vector (16, 8, 4, 2 or 1 bytes) that every pointer and stride allows.
+//
+// Reference behaviour:
+//   copy_blocks    kv_cache_manager.py:481-523 (page-by-page snapshot/restore)
+//   finalize       kernels/routing.py:147-177 (finalize_kernel), launched as in
+//                  worker/model_runner.py:1331-1346
+//   finalize_token kv_cache_manager.py:806-831
+//   gather         kv_cache_manager.py:834-854 (read)
+#include <algorithm>
+
+#include "common.h"
+
+namespace vrh {
+namespace {
+
+template <int VB>
+using raw_of = typename RawVec<VB>::type;
+
+int pick_vb(std::initializer_list<int64_t> values, std::initializer_list<const void*> ptrs) {
+  for (int vb = 16; vb > 1; vb >>= 1) {
+    bool ok = true;
+    for (int64_t s : values) ok = ok && (s % vb == 0);
+    for (const void* p : ptrs) ok = ok && ((uintptr_t)p % vb == 0);
+    if (ok) return vb;
+  }
+  return 1;
+}
+
+// ------------------------------------------------------------ block copy
+// grid.x tiles one block (kUnroll * 256 vectors per workgroup), grid.y = pair.
+constexpr int kCopyUnroll = 4;
+
+struct CopyBlocksArgs {
+  char* kc;
+  char* vc;
+  const int64_t* src;
+  const int64_t* dst;
+  int64_t block_stride;  // bytes
+  int64_t vecs;          // vectors per block
+  int64_t pair_base;
+};
+
+template <int VB>
+__global__ __launch_bounds__(256) void copy_blocks_kernel(CopyBlocksArgs a) {
+  using raw_t = raw_of<VB>;
+  const int64_t pair = a.pair_base + blockIdx.y;
+  const int64_t s = a.src[pair] * a.block_stride;
+  const int64_t d = a.dst[pair] * a.block_stride;
+  const int64_t first = (int64_t)blockIdx.x * (256 * kCopyUnroll) + threadIdx.x;
+  raw_t kr[kCopyUnroll], vr[kCopyUnroll];
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u) {
+    const int64_t i = first + u * 256;
+    if (i < a.vecs) {
+      kr[u] = __builtin_nontemporal_load(reinterpret_cast<const raw_t*>(a.kc + s) + i);
+      vr[u] = __builtin_nontemporal_load(reinterpret_cast<const raw_t*>(a.vc + s) + i);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u) {
+    const int64_t i = first + u * 256;
+    if (i < a.vecs) {
+      __builtin_nontemporal_store(kr[u], reinterpret_cast<raw_t*>(a.kc + d) + i);
+      __builtin_nontemporal_store(vr[u], reinterpret_cast<raw_t*>(a.vc + d) + i);
+    }
+  }
+}
+
+// ---------------------------------------------------- slot (token) copies
+// A "slot" is the channel_bytes of one (block, layer, token). Jobs enumerate
+// (row, target plane, layer); each thread moves one vector of K and of V.
+struct FinalizeArgs {
+  char* kc;
+  char* vc;
+  const int64_t* desc;
+  const int32_t* tables;
+  int64_t row_base;
+  int32_t planes, width, page, layers;
+  int64_t block_stride, layer_stride, token_stride;  // bytes
+  int32_t vecs;                                      // vectors per slot
+};
+
+template <int VB>
+__global__ __launch_bounds__(256) void finalize_kernel(FinalizeArgs a) {
+  using raw_t = raw_of<VB>;
+  const int64_t row = a.row_base + blockIdx.y;
+  const int target = blockIdx.z % a.planes;
+  const int layer = blockIdx.z / a.planes;
+  const int64_t slot = a.desc[row * 3 + 0];
+  const int64_t depth = a.desc[row * 3 + 1];
+  const int64_t pos = a.desc[row * 3 + 2];
+  if (target <= depth) return;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= a.vecs) return;
+  const int64_t page = pos / a.page;
+  const int64_t src = a.tables[(slot * a.planes + depth) * a.width + page];
+  const int64_t dst = a.tables[(slot * a.planes + target) * a.width + page];
+  const int64_t off = (int64_t)layer * a.layer_stride + (pos % a.page) * a.token_stride;
+  const raw_t* ks = reinterpret_cast<const raw_t*>(a.kc + src * a.block_stride + off);
+  const raw_t* vs = reinterpret_cast<const raw_t*>(a.vc + src * a.block_stride + off);
+  raw_t* kd = reinterpret_cast<raw_t*>(a.kc + dst * a.block_stride + off);
+  raw_t* vd = reinterpret_cast<raw_t*>(a.vc + dst * a.block_stride + off);
+  kd[j] = ks[j];
+  vd[j] = vs[j];
+}
+
+constexpr int kMaxTokenDst = 64;
+constexpr int kMaxTokenLayers = 256;
+
+struct FinalizeTokenArgs {
+  char* kc;
+  char* vc;
+  int64_t src;
+  int64_t block_stride, layer_stride, token_stride;
+  int64_t token_off;  // offset * token_stride
+  int32_t vecs;
+  int64_t dst[kMaxTokenDst];
+  int16_t layers[kMaxTokenLayers];
+};
+
+template <int VB>
+__global__ __launch_bounds__(256) void finalize_token_kernel(FinalizeTokenArgs a) {
+  using raw_t = raw_of<VB>;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= a.vecs) return;
+  const int64_t off = (int64_t)a.layers[blockIdx.y] * a.layer_stride + a.token_off;
+  const int64_t dst = a.dst[blockIdx.z];
+  const raw_t k = reinterpret_cast<const raw_t*>(a.kc + a.src * a.block_stride + off)[j];
+  const raw_t v = reinterpret_cast<const raw_t*>(a.vc + a.src * a.block_stride + off)[j];
+  reinterpret_cast<raw_t*>(a.kc + dst * a.block_stride + off)[j] = k;
+  reinterpret_cast<raw_t*>(a.vc + dst * a.block_stride + off)[j] = v;
+}
+
+// ---------------------------------------------------------------- gather
+struct GatherArgs {
+  char* ok;
+  char* ov;
+  const char* kc;
+  const char* vc;
+  const int32_t* table;
+  int64_t token_base;
+  int32_t page;
+  int64_t block_stride, token_stride, channel;  // bytes
+  int32_t vecs;
+};
+
+template <int VB>
+__global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
+  using raw_t = raw_of<VB>;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= a.vecs) return;
+  const int64_t t = a.token_base + blockIdx.y;
+  const int64_t blk = a.table[t / a.page];
+  const int64_t src = blk * a.block_stride + (t % a.page) * a.token_stride;
+  reinterpret_cast<raw_t*>(a.ok + t * a.channel)[j] =
+      reinterpret_cast<const raw_t*>(a.kc + src)[j];
+  reinterpret_cast<raw_t*>(a.ov + t * a.channel)[j] =
+      reinterpret_cast<const raw_t*>(a.vc + src)[j];
+}
+
+#define VRH_DISPATCH_VB(vb, KERNEL, grid, block, stream, args)                      \
+  switch (vb) {                                                                     \
+    case 16: hipLaunchKernelGGL(KERNEL<16>, grid, block, 0, stream, args); break;  \
+    case 8: hipLaunchKernelGGL(KERNEL<8>, grid, block, 0, stream, args); break;    \
+    case 4: hipLaunchKernelGGL(KERNEL<4>, grid, block, 0, stream, args); break;    \
+    case 2: hipLaunchKernelGGL(KERNEL<2>, grid, block, 0, stream, args); break;    \
+    default: hipLaunchKernelGGL(KERNEL<1>, grid, block, 0, stream, args); break;   \
+  }
+
+constexpr int64_t kMaxGridY = 65535;
+
+}  // namespace
+}  // namespace vrh
+
+using namespace vrh;
+
+extern "C" int vrh_kv_copy_blocks(void* key_cache, void* value_cache, int64_t block_stride_bytes,
+                                  int64_t block_bytes, const int64_t* src_blocks,
+                                  const int64_t* dst_blocks, int64_t n, vrh_stream_t stream) {
+  VRH_CHECK_ARG(n >= 0 && block_bytes >= 0 && block_stride_bytes >= block_bytes,
+                "vrh_kv_copy_blocks: bad sizes n=%lld block_bytes=%lld stride=%lld",
+                (long long)n, (long long)block_bytes, (long long)block_stride_bytes);
+  if (n == 0 || block_bytes == 0) return VRH_OK;
+  VRH_CHECK_ARG(key_cache && value_cache && src_blocks && dst_blocks,
+                "vrh_kv_copy_blocks: null pointer");
+  const int vb = pick_vb({block_stride_bytes, block_bytes}, {key_cache, value_cache});
+  CopyBlocksArgs a;
+  a.kc = (char*)key_cache;
+  a.vc = (char*)value_cache;
+  a.src = src_blocks;
+  a.dst = dst_blocks;
+  a.block_stride = block_stride_bytes;
+  a.vecs = block_bytes / vb;
+  const int64_t gx = ceil_div64(a.vecs, 256 * kCopyUnroll);
+  VRH_CHECK_ARG(gx < (1ll << 31), "vrh_kv_copy_blocks: block too large");
+  hipStream_t s = (hipStream_t)stream;
+  for (int64_t first = 0; first < n; first += kMaxGridY) {
+    a.pair_base = first;
+    const int64_t count = std::min(n - first, kMaxGridY);
+    dim3 grid((unsigned)gx, (unsigned)count);
+    VRH_DISPATCH_VB(vb, copy_blocks_kernel, grid, dim3(256), s, a);
+  }
+  VRH_RETURN_LAUNCH("vrh_kv_copy_blocks");
+}
+
+extern "C" int vrh_kv_finalize(void* key_cache, void* value_cache, const int64_t* descriptors,
+                               const int32_t* tables, int64_t rows, int32_t planes,
+                               int32_t width, int32_t block_size, int32_t layers,
+                               int64_t block_stride_bytes, int64_t layer_stride_bytes,
+                               int64_t token_stride_bytes, int64_t channel_bytes,
+                               vrh_stream_t stream) {
+  VRH_CHECK_ARG(rows >= 0 && planes >= 1 && width >= 1 && block_size >= 1 && layers >= 1 &&
+                    channel_bytes >= 1,
+                "vrh_kv_finalize: bad sizes");
+  VRH_CHECK_ARG((int64_t)planes * layers <= 65535, "vrh_kv_finalize: planes * layers > 65535");
+  if (rows == 0 || planes == 1) return VRH_OK;
+  VRH_CHECK_ARG(key_cache && value_cache && descriptors && tables, "vrh_kv_finalize: null pointer");
+  const int vb = pick_vb({block_stride_bytes, layer_stride_bytes, token_stride_bytes, channel_bytes},
+                         {key_cache, value_cache});
+  FinalizeArgs a;
+  a.kc = (char*)key_cache;
+  a.vc = (char*)value_cache;
+  a.desc = descriptors;
+  a.tables = tables;
+  a.planes = planes;
+  a.width = width;
+  a.page = block_size;
+  a.layers = layers;
+  a.block_stride = block_stride_bytes;
+  a.layer_stride = layer_stride_bytes;
+  a.token_stride = token_stride_bytes;
+  VRH_CHECK_ARG(channel_bytes / vb < (1ll << 30), "vrh_kv_finalize: slot too large");
+  a.vecs = (int32_t)(channel_bytes / vb);
+  hipStream_t s = (hipStream_t)stream;
+  for (int64_t first = 0; first < rows; first += kMaxGridY) {
+    a.row_base = first;
+    const int64_t count = std::min(rows - first, kMaxGridY);
+    dim3 grid((unsigned)ceil_div64(a.vecs, 256), (unsigned)count, (unsigned)(planes * layers));
+    VRH_DISPATCH_VB(vb, finalize_kernel, grid, dim3(256), s, a);
+  }
+  VRH_RETURN_LAUNCH("vrh_kv_finalize");
+}
+
+extern "C" int vrh_kv_finalize_token(void* key_cache, void* value_cache, int64_t src_block,
+                                     const int64_t* dst_blocks, int32_t num_dst, int32_t offset,
+                                     const int32_t* layer_ids, int32_t num_layers,
+                                     int64_t block_stride_bytes, int64_t layer_stride_bytes,
+                                     int64_t token_stride_bytes, int64_t channel_bytes,
+                                     vrh_stream_t stream) {
+  VRH_CHECK_ARG(num_dst >= 0 && num_dst <= kMaxTokenDst,
+                "vrh_kv_finalize_token: num_dst must be in [0, %d]", kMaxTokenDst);
+  VRH_CHECK_ARG(num_layers >= 0 && num_layers <= kMaxTokenLayers,
+                "vrh_kv_finalize_token: num_layers must be in [0, %d]", kMaxTokenLayers);
+  VRH_CHECK_ARG(channel_bytes >= 1 && offset >= 0 && src_block >= 0,
+                "vrh_kv_finalize_token: bad sizes");
+  if (num_dst == 0 || num_layers == 0) return VRH_OK;
+  VRH_CHECK_ARG(key_cache && value_cache && dst_blocks && layer_ids,
+                "vrh_kv_finalize_token: null pointer");
+  const int vb = pick_vb({block_stride_bytes, layer_stride_bytes, token_stride_bytes, channel_bytes},
+                         {key_cache, value_cache});
+  FinalizeTokenArgs a;
+  a.kc = (char*)key_cache;
+  a.vc = (char*)value_cache;
+  a.src = src_block;
+  a.block_stride = block_stride_bytes;
+  a.layer_stride = layer_stride_bytes;
+  a.token_stride = token_stride_bytes;
+  a.token_off = (int64_t)offset * token_stride_bytes;
+  VRH_CHECK_ARG(channel_bytes / vb < (1ll << 30), "vrh_kv_finalize_token: slot too large");
+  a.vecs = (int32_t)(channel_bytes / vb);
+  for (int i = 0; i < num_dst; ++i) {
+    VRH_CHECK_ARG(dst_blocks[i] >= 0 && dst_blocks[i] != src_block,
+                  "vrh_kv_finalize_token: destination %d is invalid", i);
+    a.dst[i] = dst_blocks[i];
+  }
+  for (int i = 0; i < num_layers; ++i) {
+    VRH_CHECK_ARG(layer_ids[i] >= 0 && layer_ids[i] < 32768,
+                  "vrh_kv_finalize_token: layer id %d out of range", layer_ids[i]);
+    a.layers[i] = (int16_t)layer_ids[i];
+  }
+  dim3 grid((unsigned)ceil_div64(a.vecs, 256), (unsigned)num_layers, (unsigned)num_dst);
+  VRH_DISPATCH_VB(vb, finalize_token_kernel, grid, dim3(256), (hipStream_t)stream, a);
+  VRH_RETURN_LAUNCH("vrh_kv_finalize_token");
+}
+
+extern "C" int vrh_kv_gather(void* out_k, void* out_v, const void* key_cache,
+                             const void* value_cache, const int32_t* table, int64_t length,
+                             int32_t block_size, int64_t block_stride_bytes,
+                             int64_t token_stride_bytes, int64_t channel_bytes,
+                             vrh_stream_t stream) {
+  VRH_CHECK_ARG(length >= 0 && block_size >= 1 && channel_bytes >= 1,
+                "vrh_kv_gather: bad sizes");
+  if (length == 0) return VRH_OK;
+  VRH_CHECK_ARG(out_k && out_v && key_cache && value_cache && table,
+                "vrh_kv_gather: null pointer");
+  const int vb = pick_vb({block_stride_bytes, token_stride_bytes, channel_bytes},
+                         {out_k, out_v, key_cache, value_cache});
+  GatherArgs a;
+  a.ok = (char*)out_k;
+  a.ov = (char*)out_v;
+  a.kc = (const char*)key_cache;
+  a.vc = (const char*)value_cache;
+  a.table = table;
+  a.page = block_size;
+  a.block_stride = block_stride_bytes;
+  a.token_stride = token_stride_bytes;
+  a.channel = channel_bytes;
+  VRH_CHECK_ARG(channel_bytes / vb < (1ll << 30), "vrh_kv_gather: slot too large");
+  a.vecs = (int32_t)(channel_bytes / vb);
+  hipStream_t s = (hipStream_t)stream;
+  for (int64_t first = 0; first < length; first += kMaxGridY) {
+    a.token_base = first;
+    const int64_t count = std::min(length - first, kMaxGridY);
+    dim3 grid((unsigned)ceil_div64(a.vecs, 256), (unsigned)count);
+    VRH_DISPATCH_VB(vb, gather_kernel, grid, dim3(256), s, a);
+  }
+  VRH_RETURN_LAUNCH("vrh_kv_gather");
+}
