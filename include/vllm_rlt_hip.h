@@ -107,8 +107,13 @@ int vrh_paged_decode(int dtype, void* out, const void* q, const void* key_cache,
  * Packed causal prefill, bottom-right aligned: sequence s owns query rows
  * [cu_seqlens_q[s], cu_seqlens_q[s+1]) and keys [0, context_lengths[s]) through
  * block_tables[s]; its query i sits at position n_s - q_s + i and attends keys
- * at positions <= that. bf16/f16 use MFMA with fp32 accumulation; f32 uses
- * fp32 MFMA (exact products). */
+ * at positions <= that. bf16/f16 with head_dim a multiple of 32 (<= 224) use
+ * MFMA tiles with fp32 accumulation; other cases compute each query row with
+ * the decode kernel. With a workspace of
+ * vrh_paged_prefill_workspace_bytes(num_seqs, q_heads, head_dim) bytes,
+ * sequences of one query (decode rows riding in a packed batch) use split-KV
+ * decode; with none (NULL, 0) every sequence goes through the MFMA tiles. */
+size_t vrh_paged_prefill_workspace_bytes(int64_t num_seqs, int32_t q_heads, int32_t head_dim);
 int vrh_paged_prefill(int dtype, void* out, const void* q, const void* key_cache,
                       const void* value_cache, const int32_t* block_tables,
                       const int32_t* context_lengths, const int32_t* cu_seqlens_q,
@@ -118,7 +123,7 @@ int vrh_paged_prefill(int dtype, void* out, const void* q, const void* key_cache
                       int64_t q_head_stride, int64_t out_token_stride, int64_t out_head_stride,
                       int64_t k_block_stride, int64_t k_token_stride, int64_t k_head_stride,
                       int64_t v_block_stride, int64_t v_token_stride, int64_t v_head_stride,
-                      vrh_stream_t stream);
+                      void* workspace, size_t workspace_bytes, vrh_stream_t stream);
 
 /* ------------------------------------------------------------------ gather
  * out_k[t] = K[table[t / block_size], t % block_size] for t < length (and V),

@@ -252,3 +252,26 @@ def test_empty_inputs(gpu):
     assert paged_attention(empty_q, k, k, tables, lengths).shape == (0, 2, 64)
     cu = torch.zeros(1, dtype=torch.int32, device=gpu)
     assert paged_prefill_attention(empty_q, k, k, tables, lengths, cu, 1).shape == (0, 2, 64)
+
+
+def test_prefill_without_workspace_runs_decode_rows_through_mfma_tiles(gpu):
+    """The C ABI accepts no workspace: every sequence (also q_len = 1) then goes
+    through the MFMA tiles; results match the routed (split-KV) path."""
+    from vllm_rlt.kernels._hip import library
+    from vllm_rlt.kernels.hip_attention import dtype_code, paged_prefill_attention
+
+    sequences = [(300, 1), (37, 5), (1000, 1), (129, 120), (5, 1)]
+    q, k, v, tables, lengths, cu, max_q = prefill_inputs(sequences, 8, 8, 128, torch.bfloat16,
+                                                         gpu, seed=21)
+    routed = paged_prefill_attention(q, k, v, tables, lengths, cu, max_q)
+    out = torch.empty_like(q)
+    lib = library()
+    lib.check(lib.vrh_paged_prefill(
+        dtype_code(q.dtype), out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+        tables.data_ptr(), lengths.data_ptr(), cu.data_ptr(), len(sequences), q.shape[0], max_q,
+        8, 8, 128, 16, tables.shape[1], tables.stride(0), q.stride(0), q.stride(1),
+        out.stride(0), out.stride(1), *k.stride()[:3], *v.stride()[:3], None, 0,
+        torch.cuda.current_stream().cuda_stream), "vrh_paged_prefill")
+    expected = oracle_prefill(q, k, v, tables, lengths, cu)
+    assert_close(out, expected, torch.bfloat16)
+    assert_close(routed, expected, torch.bfloat16)

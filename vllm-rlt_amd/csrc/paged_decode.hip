@@ -9,10 +9,13 @@
 //  * One 64-lane wavefront per (split, q head, row). A split is a run of whole
 //    pages: bps = max(min_bps, ceil(pages / kMaxSplits)) pages, so the
 //    partition depends only on the row's own length -> batch invariance.
+//    Short splits (64 tokens by default) keep ~36k waves in flight for the
+//    Ouro decode batch, which hides HBM latency and balances the tail.
 //  * Lane layout: LPT lanes cover one token's head_dim with VEC elements each
 //    (16-byte global loads for bf16 D=128: LPT=16), so one wave-wide load
-//    instruction fetches TPL = 64 / LPT tokens; U = 4 loads of K and 4 of V are
-//    in flight per lane per chunk.
+//    instruction fetches TPL = 64 / LPT tokens; U loads of K and U of V are
+//    issued back to back per chunk (branch-free: positions past the end
+//    re-read the last valid token and are masked).
 //  * The row's page ids for up to 64 pages sit in one VGPR (one per lane) and
 //    are fetched with ds_bpermute, so the page table is read once per split.
 //  * Each token group keeps its own online-softmax state (m, l, acc) in the
@@ -29,9 +32,34 @@
 namespace vrh {
 namespace {
 
+// Tuning knobs (compile-time): wave loads per chunk (in flight per lane for
+// each of K and V), minimum split length, next-chunk prefetch, non-temporal
+// K/V loads.
+#ifndef VRH_DECODE_U
+#define VRH_DECODE_U 4
+#endif
+#ifndef VRH_SPLIT_TOKENS
+#define VRH_SPLIT_TOKENS 64
+#endif
+#ifndef VRH_DECODE_NT
+#define VRH_DECODE_NT 1
+#endif
+#ifndef VRH_DECODE_PREFETCH
+#define VRH_DECODE_PREFETCH 1
+#endif
+
 constexpr int kMaxSplits = 32;
-constexpr int kSplitTokens = 256;  // minimum tokens per split (whole pages)
-constexpr int kU = 4;              // wave loads per chunk for each of K and V
+constexpr int kSplitTokens = VRH_SPLIT_TOKENS;  // minimum tokens per split (whole pages)
+constexpr int kU = VRH_DECODE_U;                // wave loads per chunk (K and V each)
+
+template <typename T, int VEC>
+__device__ __forceinline__ typename Vec<T, VEC>::raw_t load_kv(const T* p) {
+#if VRH_DECODE_NT
+  return load_raw_stream<T, VEC>(p);
+#else
+  return load_raw<T, VEC>(p);
+#endif
+}
 
 struct DecodeArgs {
   void* out;
@@ -50,8 +78,11 @@ struct DecodeArgs {
   // Packed-prefill expansion (null for decode): row r is query i of sequence
   // s with cu_q[s] <= r < cu_q[s+1]; it reads table row s with causal length
   // lengths[s] - q_len(s) + i + 1.
+  // expand_e > 0: row r is query r % E of sequence r / E, and only sequences
+  // with q_len <= E are processed here (the others belong to the MFMA kernel).
   const int32_t* cu_q;
   int32_t num_seqs;
+  int32_t expand_e;
   int32_t q_heads, group, head_dim, block_size, bs_shift, window, min_bps, table_width;
   float scale_log2;
 };
@@ -86,21 +117,33 @@ __device__ __forceinline__ int clamp_length(int n, const DecodeArgs& a) {
   return (int64_t)n > cap ? (int)cap : n;
 }
 
-// Visible length and table row of a query row (decode: itself).
-__device__ __forceinline__ int row_length(int64_t row, const DecodeArgs& a, int64_t* table_row) {
+// Visible length, table row and query/output row of work row `row`
+// (decode: itself); -1 when the row is not handled by this launch.
+__device__ __forceinline__ int row_length(int64_t row, const DecodeArgs& a, int64_t* table_row,
+                                          int64_t* query_row) {
   if (a.cu_q == nullptr) {
     *table_row = row;
+    *query_row = row;
     return clamp_length(a.lengths[row], a);
   }
-  int lo = 0, hi = a.num_seqs - 1;  // last s with cu_q[s] <= row
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (a.cu_q[mid] <= row) lo = mid; else hi = mid - 1;
+  int seq, i;
+  if (a.expand_e > 0) {
+    seq = (int)(row / a.expand_e);
+    i = (int)(row - (int64_t)seq * a.expand_e);
+  } else {
+    int lo = 0, hi = a.num_seqs - 1;  // last s with cu_q[s] <= row
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (a.cu_q[mid] <= row) lo = mid; else hi = mid - 1;
+    }
+    seq = lo;
+    i = (int)(row - a.cu_q[lo]);
   }
-  *table_row = lo;
-  const int q_len = a.cu_q[lo + 1] - a.cu_q[lo];
-  const int i = (int)(row - a.cu_q[lo]);
-  return clamp_length(a.lengths[lo] - q_len + i + 1, a);
+  const int q_len = a.cu_q[seq + 1] - a.cu_q[seq];
+  if (a.expand_e > 0 && (q_len > a.expand_e || i >= q_len)) return -1;
+  *table_row = seq;
+  *query_row = a.cu_q[seq] + i;
+  return clamp_length(a.lengths[seq] - q_len + i + 1, a);
 }
 
 template <typename T, int VEC, int LPT>
@@ -115,10 +158,11 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   const int head = blockIdx.y;
   const int64_t row = a.row_base + blockIdx.z;
   const int kvh = head / a.group;
-  int64_t trow;
-  const int n = row_length(row, a, &trow);
+  int64_t trow, qrow;
+  const int n = row_length(row, a, &trow, &qrow);
+  if (n < 0) return;
   const bool dvalid = dg * VEC < a.head_dim;
-  T* out = reinterpret_cast<T*>(a.out) + row * a.o_row + head * a.o_head + dg * VEC;
+  T* out = reinterpret_cast<T*>(a.out) + qrow * a.o_row + (int64_t)head * a.o_head + dg * VEC;
 
   if (n == 0) {
     if (blockIdx.x == 0 && tg == 0 && dvalid) {
@@ -134,7 +178,8 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
 
   float qf[VEC];
   {
-    const T* qp = reinterpret_cast<const T*>(a.q) + row * a.q_row + head * a.q_head + dg * VEC;
+    const T* qp = reinterpret_cast<const T*>(a.q) + qrow * a.q_row + (int64_t)head * a.q_head +
+                  dg * VEC;
     if (dvalid) {
       unpack<T, VEC>(load_raw<T, VEC>(qp), qf);
     } else {
@@ -144,8 +189,11 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < VEC; ++i) qf[i] *= a.scale_log2;
   }
-  const T* kbase = reinterpret_cast<const T*>(a.k) + kvh * a.k_head + dg * VEC;
-  const T* vbase = reinterpret_cast<const T*>(a.v) + kvh * a.v_head + dg * VEC;
+  // Lanes past head_dim read dims [0, VEC) instead (in bounds); their q is zero
+  // and they store nothing.
+  const int lane_dim = dvalid ? dg * VEC : 0;
+  const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)kvh * a.k_head + lane_dim;
+  const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)kvh * a.v_head + lane_dim;
   const int32_t* table = a.tables + trow * a.table_stride;
 
   for (int split = blockIdx.x; split < P.nsplit; split += gridDim.x) {
@@ -163,13 +211,13 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
       const int tbl = (seg + lane < b1) ? table[seg + lane] : 0;
       const int s_tb = max(tb, seg * a.block_size);
       const int s_te = min(te, (seg + 64) * a.block_size);
-      for (int p0 = s_tb; p0 < s_te; p0 += CH) {
-        raw_t kr[kU], vr[kU];
-        bool val[kU];
+      if (s_tb >= s_te) continue;
+      // Branch-free loads: positions past the end re-read the last valid token
+      // (masked out of the softmax), so a chunk is one straight run of loads.
+      auto issue = [&](int p0, raw_t (&kr)[kU], raw_t (&vr)[kU]) {
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-          const int pos = p0 + u * TPL + tg;
-          val[u] = pos < s_te;
+          const int pos = min(p0 + u * TPL + tg, s_te - 1);
           int page, off;
           if (a.bs_shift >= 0) {
             page = pos >> a.bs_shift;
@@ -178,16 +226,18 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
             page = pos / a.block_size;
             off = pos - page * a.block_size;
           }
-          const int blk = shfl_i32(tbl, val[u] ? page - seg : 0);
-          if (val[u] && dvalid) {
-            const int64_t b = (int64_t)blk;
-            kr[u] = load_raw_stream<T, VEC>(kbase + b * a.k_block + off * a.k_token);
-            vr[u] = load_raw_stream<T, VEC>(vbase + b * a.v_block + off * a.v_token);
-          } else {
-            kr[u] = raw_t{};
-            vr[u] = raw_t{};
-          }
+          const int64_t blk = shfl_i32(tbl, page - seg);
+          kr[u] = load_kv<T, VEC>(kbase + blk * a.k_block + (int64_t)off * a.k_token);
+          vr[u] = load_kv<T, VEC>(vbase + blk * a.v_block + (int64_t)off * a.v_token);
         }
+      };
+      raw_t kr[kU], vr[kU];
+      issue(s_tb, kr, vr);
+      for (int p0 = s_tb; p0 < s_te; p0 += CH) {
+#if VRH_DECODE_PREFETCH
+        raw_t kn[kU], vn[kU];
+        if (p0 + CH < s_te) issue(p0 + CH, kn, vn);
+#endif
         float s[kU];
         float mx = m;
 #pragma unroll
@@ -198,7 +248,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
           for (int i = 0; i < VEC; ++i) d = fmaf(qf[i], kf[i], d);
           d = group_sum<LPT>(d);
-          s[u] = val[u] ? d : -INFINITY;
+          s[u] = (p0 + u * TPL + tg < s_te) ? d : -INFINITY;
           mx = fmaxf(mx, s[u]);
         }
         const float safe = (mx == -INFINITY) ? 0.f : mx;
@@ -216,6 +266,15 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
           for (int i = 0; i < VEC; ++i) acc[i] = fmaf(p, vf[i], acc[i]);
         }
         m = mx;
+#if VRH_DECODE_PREFETCH
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          kr[u] = kn[u];
+          vr[u] = vn[u];
+        }
+#else
+        if (p0 + CH < s_te) issue(p0 + CH, kr, vr);
+#endif
       }
     }
 
@@ -249,15 +308,18 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
-  __shared__ float weights[kMaxSplits];
-  const int lane = threadIdx.x;
-  const int head = blockIdx.x;
+// Log-sum-exp merge of a row's split partials, one wave per (row, q head),
+// 4 waves per workgroup. Lane s holds split s's weight; each lane owns ND
+// dims and issues its partial loads 8 splits at a time, all in flight.
+template <typename T, int ND>
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int head = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (head >= a.q_heads) return;
   const int64_t row = a.row_base + blockIdx.y;
-  int64_t trow;
-  const int n = row_length(row, a, &trow);
-  if (n == 0) return;
+  int64_t trow, qrow;
+  const int n = row_length(row, a, &trow, &qrow);
+  if (n <= 0) return;
   const Partition P = partition(n, a);
   if (P.nsplit <= 1) return;
   const int64_t idx0 = (row * a.q_heads + head) * kMaxSplits;
@@ -267,23 +329,57 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   const float M = wave_max(mi);
   const float wi = live ? exp2f(mi - M) : 0.f;
   const float L = wave_sum(wi * li);
-  if (lane < kMaxSplits) weights[lane] = wi;
-  __syncthreads();
   const float inv = 1.f / fmaxf(L, 1e-30f);
-  T* out = reinterpret_cast<T*>(a.out) + row * a.o_row + head * a.o_head;
-  for (int d = lane; d < a.head_dim; d += 64) {
-    float acc = 0.f;
-    for (int s = 0; s < P.nsplit; ++s) acc = fmaf(weights[s], a.part_acc[(idx0 + s) * a.head_dim + d], acc);
-    out[d] = from_f32<T>(acc * inv);
+  const float* part = a.part_acc + idx0 * a.head_dim;
+  float acc[ND];
+#pragma unroll
+  for (int e = 0; e < ND; ++e) acc[e] = 0.f;
+  for (int s0 = 0; s0 < P.nsplit; s0 += 8) {
+    float v[8][ND];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int e = 0; e < ND; ++e) {
+        const int d = lane + 64 * e;
+        v[j][e] = (s0 + j < P.nsplit && d < a.head_dim) ? part[(int64_t)(s0 + j) * a.head_dim + d]
+                                                       : 0.f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float w =
+          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wi), s0 + j < 64 ? s0 + j : 63));
+#pragma unroll
+      for (int e = 0; e < ND; ++e) acc[e] = fmaf(w, v[j][e], acc[e]);
+    }
+  }
+  T* out = reinterpret_cast<T*>(a.out) + qrow * a.o_row + (int64_t)head * a.o_head;
+#pragma unroll
+  for (int e = 0; e < ND; ++e) {
+    const int d = lane + 64 * e;
+    if (d < a.head_dim) out[d] = from_f32<T>(acc[e] * inv);
+  }
+}
+
+template <typename T>
+void launch_merge(int head_dim, dim3 grid, hipStream_t s, const DecodeArgs& a) {
+  if (head_dim <= 64) {
+    hipLaunchKernelGGL((paged_decode_merge_kernel<T, 1>), grid, dim3(256), 0, s, a);
+  } else if (head_dim <= 128) {
+    hipLaunchKernelGGL((paged_decode_merge_kernel<T, 2>), grid, dim3(256), 0, s, a);
+  } else if (head_dim <= 256) {
+    hipLaunchKernelGGL((paged_decode_merge_kernel<T, 4>), grid, dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((paged_decode_merge_kernel<T, 8>), grid, dim3(256), 0, s, a);
   }
 }
 
 template <typename T, int VEC>
-bool launch_vec(int lpt, dim3 grid, hipStream_t s, const DecodeArgs& a) {
+bool launch_vec(int lpt, dim3 grid, dim3 block, hipStream_t s, const DecodeArgs& a) {
   switch (lpt) {
-#define VRH_LPT(L)                                                                       \
-  case L:                                                                                \
-    hipLaunchKernelGGL((paged_decode_kernel<T, VEC, L>), grid, dim3(64), 0, s, a); \
+#define VRH_LPT(L)                                                                      \
+  case L:                                                                               \
+    hipLaunchKernelGGL((paged_decode_kernel<T, VEC, L>), grid, block, 0, s, a); \
     return true;
     VRH_LPT(1)
     VRH_LPT(2)
@@ -298,13 +394,13 @@ bool launch_vec(int lpt, dim3 grid, hipStream_t s, const DecodeArgs& a) {
 }
 
 template <typename T>
-bool launch_decode(int vec, int lpt, dim3 grid, hipStream_t s, const DecodeArgs& a) {
+bool launch_decode(int vec, int lpt, dim3 grid, dim3 block, hipStream_t s, const DecodeArgs& a) {
   switch (vec) {
-    case 1: return launch_vec<T, 1>(lpt, grid, s, a);
-    case 2: return launch_vec<T, 2>(lpt, grid, s, a);
-    case 4: return launch_vec<T, 4>(lpt, grid, s, a);
+    case 1: return launch_vec<T, 1>(lpt, grid, block, s, a);
+    case 2: return launch_vec<T, 2>(lpt, grid, block, s, a);
+    case 4: return launch_vec<T, 4>(lpt, grid, block, s, a);
     case 8:
-      if constexpr (sizeof(T) == 2) return launch_vec<T, 8>(lpt, grid, s, a);
+      if constexpr (sizeof(T) == 2) return launch_vec<T, 8>(lpt, grid, block, s, a);
       return false;
     default: return false;
   }
@@ -332,7 +428,7 @@ extern "C" size_t vrh_paged_decode_workspace_bytes(int64_t rows, int32_t q_heads
 int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
                     const void* value_cache, const int32_t* block_tables,
                     const int32_t* context_lengths, const int32_t* cu_q, int32_t num_seqs,
-                    int64_t rows, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                    int32_t expand_e, int64_t rows, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
                     int32_t block_size, int32_t table_width, int64_t table_stride,
                     int64_t q_row_stride, int64_t q_head_stride, int64_t out_row_stride,
                     int64_t out_head_stride, int64_t k_block_stride, int64_t k_token_stride,
@@ -406,6 +502,7 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
   a.table_stride = table_stride;
   a.cu_q = cu_q;
   a.num_seqs = num_seqs;
+  a.expand_e = expand_e;
   a.q_heads = q_heads;
   a.group = q_heads / kv_heads;
   a.head_dim = head_dim;
@@ -428,24 +525,19 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
     const unsigned count = (unsigned)std::min<int64_t>(rows - first, 65535);
     bool ok = false;
     dim3 grid((unsigned)gx, (unsigned)q_heads, count);
+    dim3 block(64);
     switch (dtype) {
-      case VRH_DTYPE_F32: ok = launch_decode<float>(vec, lpt, grid, s, a); break;
-      case VRH_DTYPE_F16: ok = launch_decode<f16_t>(vec, lpt, grid, s, a); break;
-      case VRH_DTYPE_BF16: ok = launch_decode<bf16_t>(vec, lpt, grid, s, a); break;
+      case VRH_DTYPE_F32: ok = launch_decode<float>(vec, lpt, grid, block, s, a); break;
+      case VRH_DTYPE_F16: ok = launch_decode<f16_t>(vec, lpt, grid, block, s, a); break;
+      case VRH_DTYPE_BF16: ok = launch_decode<bf16_t>(vec, lpt, grid, block, s, a); break;
     }
     VRH_CHECK_ARG(ok, "%s: no kernel for vec=%d lanes=%d", who, vec, lpt);
     if (gx == 1) continue;  // every row is a single split: output already written
-    dim3 mgrid((unsigned)q_heads, count);
+    dim3 mgrid((unsigned)ceil_div(q_heads, 4), count);
     switch (dtype) {
-      case VRH_DTYPE_F32:
-        hipLaunchKernelGGL(paged_decode_merge_kernel<float>, mgrid, dim3(64), 0, s, a);
-        break;
-      case VRH_DTYPE_F16:
-        hipLaunchKernelGGL(paged_decode_merge_kernel<f16_t>, mgrid, dim3(64), 0, s, a);
-        break;
-      case VRH_DTYPE_BF16:
-        hipLaunchKernelGGL(paged_decode_merge_kernel<bf16_t>, mgrid, dim3(64), 0, s, a);
-        break;
+      case VRH_DTYPE_F32: launch_merge<float>(head_dim, mgrid, s, a); break;
+      case VRH_DTYPE_F16: launch_merge<f16_t>(head_dim, mgrid, s, a); break;
+      case VRH_DTYPE_BF16: launch_merge<bf16_t>(head_dim, mgrid, s, a); break;
     }
   }
   VRH_RETURN_LAUNCH(who);
@@ -464,7 +556,7 @@ extern "C" int vrh_paged_decode(int dtype, void* out, const void* q, const void*
                                 size_t workspace_bytes, vrh_stream_t stream) {
   VRH_CHECK_ARG(rows == 0 || workspace != nullptr, "vrh_paged_decode: workspace is required");
   return vrh_decode_rows(dtype, out, q, key_cache, value_cache, block_tables, context_lengths,
-                         nullptr, 0, rows, q_heads, kv_heads, head_dim, block_size, table_width,
+                         nullptr, 0, 0, rows, q_heads, kv_heads, head_dim, block_size, table_width,
                          table_stride, q_row_stride, q_head_stride, out_row_stride,
                          out_head_stride, k_block_stride, k_token_stride, k_head_stride,
                          v_block_stride, v_token_stride, v_head_stride, window, workspace,

@@ -31,7 +31,7 @@
 int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
                     const void* value_cache, const int32_t* block_tables,
                     const int32_t* context_lengths, const int32_t* cu_q, int32_t num_seqs,
-                    int64_t rows, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                    int32_t expand_e, int64_t rows, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
                     int32_t block_size, int32_t table_width, int64_t table_stride,
                     int64_t q_row_stride, int64_t q_head_stride, int64_t out_row_stride,
                     int64_t out_head_stride, int64_t k_block_stride, int64_t k_token_stride,
@@ -91,6 +91,7 @@ struct PrefillArgs {
   int64_t table_stride;
   int64_t seq_base;
   int32_t group, block_size, bs_shift, table_width;
+  int32_t skip_q;  // sequences with q_len <= skip_q are left to the decode kernel
   float scale_log2;
 };
 
@@ -128,7 +129,7 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
   const int kvh = head / a.group;
   const int q_begin = a.cu[seq];
   const int q_len = a.cu[seq + 1] - q_begin;
-  if ((int)blockIdx.x * kBM >= q_len) return;
+  if ((int)blockIdx.x * kBM >= q_len || q_len <= a.skip_q) return;
   int n = a.lengths[seq];
   {
     const int64_t cap = (int64_t)a.table_width * a.block_size;
@@ -162,8 +163,11 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
 
   u32x4 kreg[KLOADS];
   u32x4 vreg[VLOADS][4];
-  auto page_of = [&](int pos, int& off) -> int64_t {
-    int page;
+  // Page ids of the keys this thread stages, fetched one tile ahead of the
+  // K/V loads so those never wait on a page-table read.
+  int32_t kpg[KLOADS];
+  int32_t vpg[VLOADS][4];
+  auto split_pos = [&](int pos, int& page, int& off) {
     if (a.bs_shift >= 0) {
       page = pos >> a.bs_shift;
       off = pos & (a.block_size - 1);
@@ -171,7 +175,27 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
       page = pos / a.block_size;
       off = pos - page * a.block_size;
     }
-    return (int64_t)table[page];
+  };
+  auto fetch_pages = [&](int t0) {
+#pragma unroll
+    for (int r = 0; r < KLOADS; ++r) {
+      const int key = (tid + 256 * r) / KCH;
+      const int pos = t0 + key;
+      int page, off;
+      split_pos(pos, page, off);
+      kpg[r] = pos < end ? table[page] : 0;
+    }
+#pragma unroll
+    for (int r = 0; r < VLOADS; ++r) {
+      const int kq = (tid + 256 * r) / KCH;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int pos = t0 + 4 * kq + j;
+        int page, off;
+        split_pos(pos, page, off);
+        vpg[r][j] = (tid + 256 * r < VUNITS && pos < end) ? table[page] : 0;
+      }
+    }
   };
   // Global -> registers for the tile starting at key t0 (zeros past `end`).
   auto fetch = [&](int t0) {
@@ -181,10 +205,10 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
       const int key = c / KCH, dc = c % KCH;
       const int pos = t0 + key;
       if (pos < end) {
-        int off;
-        const int64_t blk = page_of(pos, off);
-        kreg[r] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(kg + blk * a.k_block + off * a.k_token + dc * 8));
+        int page, off;
+        split_pos(pos, page, off);
+        kreg[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            kg + (int64_t)kpg[r] * a.k_block + off * a.k_token + dc * 8));
       } else {
         kreg[r] = u32x4{0, 0, 0, 0};
       }
@@ -197,10 +221,10 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
       for (int j = 0; j < 4; ++j) {
         const int pos = t0 + 4 * kq + j;
         if (u < VUNITS && pos < end) {
-          int off;
-          const int64_t blk = page_of(pos, off);
-          vreg[r][j] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4*>(vg + blk * a.v_block + off * a.v_token + dc * 8));
+          int page, off;
+          split_pos(pos, page, off);
+          vreg[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+              vg + (int64_t)vpg[r][j] * a.v_block + off * a.v_token + dc * 8));
         } else {
           vreg[r][j] = u32x4{0, 0, 0, 0};
         }
@@ -234,12 +258,19 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
     }
   };
 
-  if (end > 0) fetch(0);
+  if (end > 0) {
+    fetch_pages(0);
+    fetch(0);
+    if (kBN < end) fetch_pages(kBN);
+  }
   for (int t0 = 0; t0 < end; t0 += kBN) {
     __syncthreads();  // previous tile fully consumed
     stash();
     __syncthreads();
-    if (t0 + kBN < end) fetch(t0 + kBN);  // in flight while we compute
+    if (t0 + kBN < end) {
+      fetch(t0 + kBN);  // in flight while we compute
+      if (t0 + 2 * kBN < end) fetch_pages(t0 + 2 * kBN);
+    }
 
     // S^T tiles: st[kt] holds keys t0 + 16kt + 4grp + j for query `col`.
     f32x4 st[kBN / 16];
@@ -341,6 +372,15 @@ bool launch_prefill(int d, dim3 grid, hipStream_t s, const PrefillArgs& a) {
 
 using namespace vrh;
 
+// Sequences with at most this many queries (decode rows riding in a packed
+// batch) run through the split-KV decode kernel instead of 64-query MFMA tiles.
+constexpr int kDecodeQ = 1;
+
+extern "C" size_t vrh_paged_prefill_workspace_bytes(int64_t num_seqs, int32_t q_heads,
+                                                    int32_t head_dim) {
+  return vrh_paged_decode_workspace_bytes(num_seqs * kDecodeQ, q_heads, head_dim);
+}
+
 extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void* key_cache,
                                  const void* value_cache, const int32_t* block_tables,
                                  const int32_t* context_lengths, const int32_t* cu_seqlens_q,
@@ -351,13 +391,13 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
                                  int64_t out_token_stride, int64_t out_head_stride,
                                  int64_t k_block_stride, int64_t k_token_stride,
                                  int64_t k_head_stride, int64_t v_block_stride,
-                                 int64_t v_token_stride, int64_t v_head_stride,
-                                 vrh_stream_t stream) {
+                                 int64_t v_token_stride, int64_t v_head_stride, void* workspace,
+                                 size_t workspace_bytes, vrh_stream_t stream) {
   VRH_CHECK_ARG(num_seqs >= 0 && total_q >= 0 && max_seqlen_q >= 0,
                 "vrh_paged_prefill: bad sizes");
   VRH_CHECK_ARG(q_heads >= 1 && kv_heads >= 1 && q_heads % kv_heads == 0,
                 "vrh_paged_prefill: query heads must be a positive multiple of KV heads");
-  VRH_CHECK_ARG(num_seqs < (1ll << 31), "vrh_paged_prefill: too many sequences");
+  VRH_CHECK_ARG(num_seqs < (1ll << 31) / kDecodeQ, "vrh_paged_prefill: too many sequences");
   if (num_seqs == 0 || total_q == 0) return VRH_OK;
   VRH_CHECK_ARG(out && q && key_cache && value_cache && block_tables && context_lengths &&
                     cu_seqlens_q,
@@ -372,14 +412,17 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   for (const void* p : {(const void*)out, q, key_cache, value_cache}) mfma = mfma && ((uintptr_t)p % 16 == 0);
   if (!mfma) {
     return vrh_decode_rows(dtype, out, q, key_cache, value_cache, block_tables, context_lengths,
-                           cu_seqlens_q, (int32_t)num_seqs, total_q, q_heads, kv_heads, head_dim,
-                           block_size, table_width, table_stride, q_token_stride, q_head_stride,
-                           out_token_stride, out_head_stride, k_block_stride, k_token_stride,
-                           k_head_stride, v_block_stride, v_token_stride, v_head_stride, 0,
-                           nullptr, 0, s, "vrh_paged_prefill");
+                           cu_seqlens_q, (int32_t)num_seqs, 0, total_q, q_heads, kv_heads,
+                           head_dim, block_size, table_width, table_stride, q_token_stride,
+                           q_head_stride, out_token_stride, out_head_stride, k_block_stride,
+                           k_token_stride, k_head_stride, v_block_stride, v_token_stride,
+                           v_head_stride, 0, nullptr, 0, s, "vrh_paged_prefill");
   }
   VRH_CHECK_ARG(max_seqlen_q >= 1, "vrh_paged_prefill: max_seqlen_q must be positive");
   VRH_CHECK_ARG(q_heads <= 65535, "vrh_paged_prefill: too many heads");
+  const bool route_decode =
+      workspace != nullptr &&
+      workspace_bytes >= vrh_paged_prefill_workspace_bytes(num_seqs, q_heads, head_dim);
   PrefillArgs a;
   a.out = out;
   a.q = q;
@@ -403,6 +446,7 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   a.block_size = block_size;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.table_width = table_width;
+  a.skip_q = route_decode ? kDecodeQ : 0;
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
   const unsigned qblocks = (unsigned)ceil_div(max_seqlen_q, kBM);
   for (int64_t first = 0; first < num_seqs; first += 65535) {
@@ -412,6 +456,16 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
     const bool ok = dtype == VRH_DTYPE_BF16 ? launch_prefill<bf16_t>(head_dim, grid, s, a)
                                             : launch_prefill<f16_t>(head_dim, grid, s, a);
     VRH_CHECK_ARG(ok, "vrh_paged_prefill: no kernel for head_dim %d", head_dim);
+  }
+  if (route_decode) {
+    // Decode rows of the packed batch: split-KV single-query kernel.
+    const int rc = vrh_decode_rows(
+        dtype, out, q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
+        (int32_t)num_seqs, kDecodeQ, num_seqs * kDecodeQ, q_heads, kv_heads, head_dim,
+        block_size, table_width, table_stride, q_token_stride, q_head_stride, out_token_stride,
+        out_head_stride, k_block_stride, k_token_stride, k_head_stride, v_block_stride,
+        v_token_stride, v_head_stride, 0, workspace, workspace_bytes, s, "vrh_paged_prefill");
+    if (rc != VRH_OK) return rc;
   }
   VRH_RETURN_LAUNCH("vrh_paged_prefill");
 }

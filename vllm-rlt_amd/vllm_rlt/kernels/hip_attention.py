@@ -136,6 +136,8 @@ def paged_prefill_attention(q, key_cache, value_cache, block_tables, context_len
         return output
     cu_seqlens_q = cu_seqlens_q.contiguous()
     lib = library()
+    nbytes = lib.vrh_paged_prefill_workspace_bytes(sequences, q.shape[1], q.shape[2])
+    workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
     lib.check(
         lib.vrh_paged_prefill(
             dtype_code(q.dtype), output.data_ptr(), q.data_ptr(), key_cache.data_ptr(),
@@ -143,7 +145,8 @@ def paged_prefill_attention(q, key_cache, value_cache, block_tables, context_len
             cu_seqlens_q.data_ptr(), sequences, q.shape[0], int(max_seqlen_q), q.shape[1],
             key_cache.shape[2], q.shape[2], key_cache.shape[1], block_tables.shape[1],
             block_tables.stride(0), q.stride(0), q.stride(1), output.stride(0), output.stride(1),
-            *key_cache.stride()[:3], *value_cache.stride()[:3], _stream(q),
+            *key_cache.stride()[:3], *value_cache.stride()[:3], workspace.data_ptr(), nbytes,
+            _stream(q),
         ),
         "vrh_paged_prefill",
     )
