@@ -28,6 +28,19 @@ for _path in (ROOT, os.path.join(ROOT, "vllm-rlt_amd")):
         sys.path.insert(0, _path)
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_decode_config2.md")
+
+
+def profiled_traffic():
+    """HBM bytes per decode call from the committed rocprof PMC summary (scaled
+    FETCH_SIZE + WRITE_SIZE of the split and merge kernels), or None."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_call:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -38,9 +51,31 @@ def parse_args():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--skip-extras", action="store_true",
                         help="only the decode step (no append/prefill/cpu legs)")
-    parser.add_argument("--cpu-seconds", type=float, default=15.0,
+    parser.add_argument("--cpu-seconds", type=float, default=10.0,
                         help="budget of the CPU baseline sample")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run vrh_kv_copy_blocks over a known byte count (the "
+                             "reference kernel for scaling rocprof FETCH_SIZE/WRITE_SIZE)")
     return parser.parse_args()
+
+
+def copy_calibration():
+    """Copy 512 blocks of 1 MiB each (K and V): 1 GiB read + 1 GiB written per
+    launch, 5 launches. Prints the byte counts the counters should report."""
+    import torch
+
+    from vllm_rlt.kernels.hip_attention import kv_copy_blocks
+
+    device = torch.device("cuda:0")
+    pool_k = torch.zeros((1024, 1 << 19), dtype=torch.bfloat16, device=device)
+    pool_v = torch.zeros_like(pool_k)
+    src = torch.arange(0, 512, dtype=torch.int64, device=device)
+    dst = src + 512
+    for _ in range(5):
+        kv_copy_blocks(pool_k, pool_v, src, dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration": {"read_bytes": 2 * 512 * (1 << 20),
+                                           "write_bytes": 2 * 512 * (1 << 20)}}))
 
 
 def event_time_ms(fn, repeats):
@@ -57,8 +92,35 @@ def event_time_ms(fn, repeats):
     return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / repeats
 
 
+def graph_time_ms(fn, replays):
+    """Kernel time of ``fn`` without Python launch overhead: capture it once in
+    a HIP graph and time ``replays`` back-to-back replays with HIP events."""
+    import torch
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fn()  # warm up outside capture (library load, allocator)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / replays
+
+
 def cpu_baseline(work, budget_s):
-    """Oracle decode (numpy, 1 thread) on a bounded sample of rows of layer 0."""
+    """Oracle decode (numpy, 1 thread) on a bounded sample: whole layers of the
+    config-2 batch, layer after layer, until ``budget_s`` of CPU time."""
     import numpy as np
     import torch
 
@@ -67,22 +129,23 @@ def cpu_baseline(work, budget_s):
     rows = work.rows
     tables = work.block_tables.cpu()
     lengths = work.context_lengths.cpu()
-    kc, vc = work.key_cache[:, 0], work.value_cache[:, 0]
-    es = kc.element_size()
-    hkv, d = kc.shape[2], kc.shape[3]
-    done_bytes, elapsed, sampled = 0, 0.0, 0
-    for row in range(rows):
-        n = int(lengths[row])
-        pages = tables[row, : -(-n // 16)].to(torch.int64)
-        k_rows = kc[pages.to(kc.device)].float().cpu().numpy()
-        v_rows = vc[pages.to(kc.device)].float().cpu().numpy()
-        local = np.arange(len(pages), dtype=np.int32)[None]
-        q = work.q[row : row + 1].float().cpu().numpy()
-        t0 = time.perf_counter()
-        ref.paged_attention(q, k_rows, v_rows, local, np.array([n], np.int32))
-        elapsed += time.perf_counter() - t0
-        done_bytes += n * 2 * hkv * d * es + 2 * q.size * es + len(pages) * 4
-        sampled += 1
+    es = work.key_cache.element_size()
+    hkv, d = work.key_cache.shape[3], work.key_cache.shape[4]
+    done_bytes, elapsed, layers_done = 0, 0.0, 0
+    for layer in range(work.layers):
+        kc, vc = work.key_cache[:, layer], work.value_cache[:, layer]
+        for row in range(rows):
+            n = int(lengths[row])
+            pages = tables[row, : -(-n // 16)].to(torch.int64).to(kc.device)
+            k_rows = kc[pages].float().cpu().numpy()
+            v_rows = vc[pages].float().cpu().numpy()
+            local = np.arange(len(pages), dtype=np.int32)[None]
+            q = work.q[row : row + 1].float().cpu().numpy()
+            t0 = time.perf_counter()
+            ref.paged_attention(q, k_rows, v_rows, local, np.array([n], np.int32))
+            elapsed += time.perf_counter() - t0
+            done_bytes += n * 2 * hkv * d * es + 2 * q.size * es + len(pages) * 4
+        layers_done += 1
         if elapsed > budget_s:
             break
     return {
@@ -90,8 +153,8 @@ def cpu_baseline(work, budget_s):
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"numpy oracle decode of {sampled}/{rows} config-2 rows of one layer "
-                  f"({elapsed:.1f} s)",
+        "sample": f"numpy oracle decode of all {rows} config-2 rows for {layers_done} of "
+                  f"{work.layers} layers ({elapsed:.1f} s of CPU compute, 1 thread)",
     }
 
 
@@ -101,6 +164,9 @@ def main():
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); this build has no "
               "multi-GPU path", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     import torch
 
     from vllm_rlt import workloads
@@ -128,19 +194,23 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    start_ev = torch.cuda.Event(enable_timing=True)
+    end_ev = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    start_ev.record()
     for _ in range(args.steps):
         step()
+    end_ev.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # HIP-event time of the timed region on the stream the kernels run on;
+    # one decode call = split kernel + merge kernel.
+    call_ms = start_ev.elapsed_time(end_ev) / (args.steps * layers)
     ms_per_step = wall * 1e3 / args.steps
     decode_bytes = work.decode_bytes()
     step_bytes = decode_bytes * layers
     value = step_bytes / (wall / args.steps) / 1e9
 
-    # HIP-event time of one decode call (split kernel + merge), same stream.
-    call_ms = event_time_ms(lambda: paged_attention(q, kviews[0], vviews[0], tables, lengths),
-                            max(20, args.steps))
     achieved = decode_bytes / (call_ms * 1e-3) / 1e9
     result = {
         "metric": "paged-decode KV GB/s (% of HBM peak) + KV-append GB/s, Ouro-1.4B shape",
@@ -171,34 +241,34 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "paged_decode_kernel<bf16,8,16> + paged_decode_merge_kernel",
+            "traffic": profiled_traffic(),
+            "kernel": "paged_decode_kernel<bf16,8,16> + paged_decode_merge_kernel<bf16,2> "
+                      "(one decode call)",
             "call_ms": round(call_ms, 5),
         },
     }
 
     if not args.skip_extras:
         # 24-layer batched append of the step's 64 tokens (one launch).
-        append_layers_ms = event_time_ms(
+        append_layers_ms = graph_time_ms(
             lambda: kv_append_layers(work.key_cache, work.value_cache, 0, work.k_new, work.v_new,
-                                     work.write_blocks, work.write_offsets), 50)
+                                     work.write_blocks, work.write_offsets), 100)
         append_layers_bytes = work.append_bytes(layers)
         # single-layer decode append (latency)
-        single_ms = event_time_ms(
+        single_ms = graph_time_ms(
             lambda: kv_append(kviews[0], vviews[0], work.k_new[0], work.v_new[0],
-                              work.write_blocks, work.write_offsets), 50)
-        del kviews, vviews
+                              work.write_blocks, work.write_offsets), 100)
         extras = {"append_24_layers": {
             "gbs": round(append_layers_bytes / (append_layers_ms * 1e-3) / 1e9, 2),
             "us": round(append_layers_ms * 1e3, 2), "bytes": append_layers_bytes},
             "append_one_layer_us": round(single_ms * 1e3, 2)}
         result["cpu_baseline"] = cpu_baseline(work, args.cpu_seconds)
-        del work
+        del work, kviews, vviews
         torch.cuda.empty_cache()
         pw = workloads.config4(device=device)
         kc, vc = pw.key_cache[:, 0], pw.value_cache[:, 0]
-        append_ms = event_time_ms(
-            lambda: kv_append(kc, vc, pw.k_new, pw.v_new, pw.write_blocks, pw.write_offsets), 50)
+        append_ms = graph_time_ms(
+            lambda: kv_append(kc, vc, pw.k_new, pw.v_new, pw.write_blocks, pw.write_offsets), 100)
         prefill_ms = event_time_ms(
             lambda: paged_prefill_attention(pw.q, kc, vc, pw.block_tables, pw.context_lengths,
                                             pw.cu_seqlens_q, pw.max_seqlen_q), 10)
