@@ -2,7 +2,7 @@
 //
 // Storage types: float (f32), _Float16 (f16) and bf16 kept as raw uint16_t bits.
 // Every kernel computes in fp32 and converts on load/store; bf16 stores round to
-// nearest even, which is what torch's `.to(torch.bfloat16)` does.
+// nearest even (hardware v_cvt_pk_bf16_f32), as torch's `.to(torch.bfloat16)`.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -32,16 +32,31 @@ template <>
 __device__ __forceinline__ f16_t from_f32<f16_t>(float x) { return (f16_t)x; }
 template <>
 __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
-  uint32_t u = __float_as_uint(x);
+  // v_cvt_pk_bf16_f32: round to nearest even, NaN stays NaN.
   bf16_t r;
-  if ((u & 0x7fffffffu) > 0x7f800000u) {  // NaN: keep it quiet, keep the sign
-    r.bits = (uint16_t)((u >> 16) | 0x0040u);
-  } else {
-    u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest, ties to even
-    r.bits = (uint16_t)(u >> 16);
-  }
+  r.bits = __builtin_bit_cast(uint16_t, (__bf16)x);
   return r;
 }
+
+// Two floats to packed 16-bit storage (low half = lo), one conversion.
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2<bf16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t));
+}
+
+// v_exp_f32 (2^x) and v_rcp_f32 without library range handling: softmax
+// arguments are <= 0 (or -inf -> 0) and the reciprocal's input is >= 1e-30.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
 // ---------------------------------------------------------------- raw vectors
 // A VEC-element vector of T loaded/stored as one global instruction

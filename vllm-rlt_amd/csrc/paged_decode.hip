@@ -252,13 +252,13 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
           mx = fmaxf(mx, s[u]);
         }
         const float safe = (mx == -INFINITY) ? 0.f : mx;
-        const float corr = exp2f(m - safe);
+        const float corr = fast_exp2(m - safe);
         l *= corr;
 #pragma unroll
         for (int i = 0; i < VEC; ++i) acc[i] *= corr;
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-          const float p = exp2f(s[u] - safe);
+          const float p = fast_exp2(s[u] - safe);
           l += p;
           float vf[VEC];
           unpack<T, VEC>(vr[u], vf);
@@ -280,14 +280,14 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
 
     // Merge the token groups' states (fixed butterfly order).
     const float M = cross_group_max<LPT>(m);
-    const float w = (m == -INFINITY) ? 0.f : exp2f(m - M);
+    const float w = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
     const float L = cross_group_sum<LPT>(l * w);
 #pragma unroll
     for (int i = 0; i < VEC; ++i) acc[i] = cross_group_sum<LPT>(acc[i] * w);
 
     if (P.nsplit == 1) {
       if (tg == 0 && dvalid) {
-        const float inv = 1.f / fmaxf(L, 1e-30f);
+        const float inv = fast_rcp(fmaxf(L, 1e-30f));
         float o[VEC];
 #pragma unroll
         for (int i = 0; i < VEC; ++i) o[i] = acc[i] * inv;
@@ -327,9 +327,9 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   const float mi = live ? a.part_ml[(idx0 + lane) * 2 + 0] : -INFINITY;
   const float li = live ? a.part_ml[(idx0 + lane) * 2 + 1] : 0.f;
   const float M = wave_max(mi);
-  const float wi = live ? exp2f(mi - M) : 0.f;
+  const float wi = live ? fast_exp2(mi - M) : 0.f;
   const float L = wave_sum(wi * li);
-  const float inv = 1.f / fmaxf(L, 1e-30f);
+  const float inv = fast_rcp(fmaxf(L, 1e-30f));
   const float* part = a.part_acc + idx0 * a.head_dim;
   float acc[ND];
 #pragma unroll

@@ -7,20 +7,20 @@
 // dtype before the PV product (as the reference's `weights.to(values.dtype)`).
 //
 // MFMA path (bf16/f16, head_dim a multiple of 32 up to 224, LDS-bound):
-//  * Workgroup = 4 waves = 64 query rows of one (sequence, q head); each wave
-//    owns 16 queries. K/V tiles of 64 keys are staged in LDS once per
-//    workgroup and shared by the 4 waves; the next tile is prefetched into
-//    registers while the current one is consumed.
-//  * S^T = K Q^T with v_mfma_f32_16x16x32_{bf16,f16}: A = K rows from LDS
+//  * Workgroup = 4 waves = 128 query rows of one (sequence, q head); each wave
+//    owns 32 queries. K/V tiles of 64 keys are staged in LDS (two stages) and
+//    shared by the 4 waves: tile t is consumed while tile t+1 sits in the other
+//    stage and tile t+2 is in flight into registers; one barrier per tile.
+//  * S^T = K Q^T with v_mfma_f32_32x32x16_{bf16,f16}: A = K rows from LDS
 //    (16-byte reads), B = Q^T held in registers for the whole kernel.
-//    Output lane l holds query l % 16 and keys 4 * (l / 16) + j, j < 4.
+//    Output lane l holds query l % 32 and keys 8 * (j / 4) + 4 * (l / 32) + j % 4.
 //  * O^T = V^T P^T: the S^T accumulator of a lane is already a P^T B-operand
 //    (same query column, keys in the lane's k-slots), so P never goes through
 //    LDS. V is stored transposed in LDS ([d][key]) when the tile is staged; A
 //    reads are two 8-byte reads whose keys match the P^T k-slots. Only the
 //    pairing of A and B k-slots matters, not the hardware's k order.
-//  * Per-query running max is reduced over the 4 lane groups each tile; the
-//    running sum stays a per-lane partial until the end.
+//  * Per-query running max is reduced over the lane pair (l, l ^ 32) each
+//    tile; the running sum stays a per-lane partial until the end.
 // Other dtypes / head dims (f32 reference checks, odd dims) run the decode
 // kernel over the expanded rows: query i of sequence s is a decode row with
 // length n_s - q_s + i + 1 (the per-row formulation the reference tests use).
@@ -42,40 +42,47 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
 namespace vrh {
 namespace {
 
-constexpr int kBM = 64;  // queries per workgroup (16 per wave)
-constexpr int kBN = 64;  // keys per tile
+#ifndef VRH_PREFILL_WAVES
+#define VRH_PREFILL_WAVES 4
+#endif
+#ifndef VRH_PREFILL_BN
+#define VRH_PREFILL_BN 64
+#endif
+constexpr int kWaves = VRH_PREFILL_WAVES;  // waves per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr int kWQ = 32;                    // queries per wave
+constexpr int kBM = kWQ * kWaves;          // queries per workgroup
+constexpr int kBN = VRH_PREFILL_BN;        // keys per tile
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
-typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 
+// 32x32x16 MFMA: A lane l = row l % 32 with k-slots 8 * (l / 32) + i, B lane
+// l = column l % 32 with the same k-slots; D lane l = column l % 32, element j
+// = row 8 * (j / 4) + 4 * (l / 32) + j % 4.
 template <typename T>
 struct Mfma;
 template <>
 struct Mfma<bf16_t> {
-  __device__ static f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+  __device__ static f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
 };
 template <>
 struct Mfma<f16_t> {
-  __device__ static f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+  __device__ static f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
 };
 
-__device__ __forceinline__ uint32_t bits16(bf16_t x) { return x.bits; }
-__device__ __forceinline__ uint32_t bits16(f16_t x) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, x);
-}
-template <typename T>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return bits16(from_f32<T>(lo)) | (bits16(from_f32<T>(hi)) << 16);
-}
+// K/V tiles are re-read by every query block of a sequence: normal (cached)
+// loads, so the XCD's L2 serves the repeats.
+__device__ __forceinline__ u32x4 load_cached(const u32x4* p) { return *p; }
 
 struct PrefillArgs {
   void* out;
@@ -89,73 +96,100 @@ struct PrefillArgs {
   int64_t k_block, k_token, k_head;
   int64_t v_block, v_token, v_head;
   int64_t table_stride;
-  int64_t seq_base;
+  int64_t num_seqs;
+  int32_t qblocks, kv_heads;
   int32_t group, block_size, bs_shift, table_width;
   int32_t skip_q;  // sequences with q_len <= skip_q are left to the decode kernel
   float scale_log2;
 };
 
-// LDS row pitches (elements): +8 / +4 padding breaks bank aliasing of the
-// 16-lane row reads.
+// LDS tiles, two stages each. Row pitches (elements) are padded by 16 bytes so
+// the 32 rows an MFMA operand read touches spread over the banks.
 template <int D>
 struct Lds {
-  static constexpr int kPitch = D + 8;     // K tile [kBN][kPitch]
-  static constexpr int vPitch = kBN + 4;   // V^T tile [D][vPitch]
+  static constexpr int kPitch = D + 8;    // K tile [kBN][kPitch]
+  static constexpr int vPitch = kBN + 8;  // V^T tile [D][vPitch]
   static constexpr int kElems = kBN * kPitch;
   static constexpr int vElems = D * vPitch;
 };
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
-  constexpr int DC = D / 32;         // 32-wide d chunks (QK^T k-steps)
-  constexpr int DT = D / 16;         // 16-row d tiles of O^T
-  constexpr int KCH = D / 8;         // 16-byte chunks per K row
-  constexpr int KLOADS = kBN * KCH / 256;   // K tile vectors per thread
-  constexpr int VUNITS = (kBN / 4) * KCH;   // (4 keys x 8 dims) units per V tile
-  constexpr int VLOADS = (VUNITS + 255) / 256;
-  static_assert(D % 32 == 0 && D <= 256, "head_dim");
-  static_assert(kBN * KCH % 256 == 0, "K tile split");
+#ifndef VRH_PREFILL_WG_PER_CU
+#define VRH_PREFILL_WG_PER_CU 2
+#endif
 
-  __shared__ __attribute__((aligned(16))) uint16_t ks[Lds<D>::kElems];
-  __shared__ __attribute__((aligned(16))) uint16_t vts[Lds<D>::vElems];
+// Page addressing modes: kDiv (any block size), kShift (power of two), kGroup
+// (power of two >= 16: a 16-key group never straddles a page, so the four
+// group base addresses of a tile are wave-uniform scalars).
+enum PageMode { kDiv = 0, kShift = 1, kGroup = 2 };
+
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill_kernel(PrefillArgs a) {
+  constexpr int DC = D / 16;                // 16-wide d chunks (QK^T k-steps)
+  constexpr int DB = D / 32;                // 32-row d blocks of O^T
+  constexpr int KCH = D / 8;                // 16-byte chunks per K row
+  constexpr int KVECS = kBN * KCH;               // K tile 16-byte vectors
+  constexpr int KLOADS = (KVECS + kThreads - 1) / kThreads;  // per thread
+  constexpr int VUNITS = (kBN / 4) * KCH;       // (4 keys x 8 dims) units per V tile
+  constexpr int VLOADS = (VUNITS + kThreads - 1) / kThreads;
+  static_assert(D % 32 == 0 && D <= 224, "head_dim");
+
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][Lds<D>::kElems];
+  __shared__ __attribute__((aligned(16))) uint16_t vts[2][Lds<D>::vElems];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int col = lane & 15;  // query column within the wave's 16
-  const int grp = lane >> 4;  // lane group 0..3
-  const int64_t seq = a.seq_base + blockIdx.z;
-  const int head = blockIdx.y;
+  const int col = lane & 31;  // query column of this lane
+  const int half = lane >> 5; // k-slot half (0 or 1)
+  // XCD-aware order: workgroup ids are dealt round-robin to the 8 XCDs (id L
+  // runs on XCD L % 8). A group = one (sequence, kv head); its work items --
+  // every query block of every q head reading that K/V -- all go to XCD
+  // group % 8, back to back, so their K/V tiles are shared in that XCD's L2.
+  // Within a group the longest (last) query blocks run first.
+  const int per_group = a.group * a.qblocks;
+  const int64_t slot = blockIdx.x / 8;
+  const int64_t g = (slot / per_group) * 8 + blockIdx.x % 8;
+  if (g >= a.num_seqs * a.kv_heads) return;
+  const int r_item = (int)(slot % per_group);
+  const int64_t seq = g / a.kv_heads;
+  const int head = (int)(g % a.kv_heads) * a.group + r_item / a.qblocks;
+  const int qb = a.qblocks - 1 - r_item % a.qblocks;
   const int kvh = head / a.group;
   const int q_begin = a.cu[seq];
   const int q_len = a.cu[seq + 1] - q_begin;
-  if ((int)blockIdx.x * kBM >= q_len || q_len <= a.skip_q) return;
+  if (qb * kBM >= q_len || q_len <= a.skip_q) return;
   int n = a.lengths[seq];
   {
     const int64_t cap = (int64_t)a.table_width * a.block_size;
     n = n < 0 ? 0 : ((int64_t)n > cap ? (int)cap : n);
   }
   const int prefix = n - q_len;
-  const int qi = blockIdx.x * kBM + wave * 16 + col;  // this lane's query
+  const int qi = qb * kBM + wave * kWQ + col;  // this lane's query
   const bool q_ok = qi < q_len;
   const int qpos = prefix + qi;
-  const int end = max(0, min(n, prefix + ((int)blockIdx.x + 1) * kBM));
+  const int wave_qpos0 = prefix + qb * kBM + wave * kWQ;
+  const int end = max(0, min(n, prefix + (qb + 1) * kBM));
+  const int tiles = (end + kBN - 1) / kBN;
   const int32_t* table = a.tables + seq * a.table_stride;
 
-  // Q^T B-operands: lane holds query `col`, dims 32c + 8*grp .. +8.
+  // Q^T B-operands: lane holds query `col`, dims 16c + 8*half .. +8.
   u32x4 qop[DC];
   {
-    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)(q_begin + qi) * a.q_token +
-                  head * a.q_head + 8 * grp;
+    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)(q_begin + (q_ok ? qi : 0)) * a.q_token +
+                  head * a.q_head + 8 * half;
 #pragma unroll
-    for (int c = 0; c < DC; ++c)
-      qop[c] = q_ok ? *reinterpret_cast<const u32x4*>(qp + 32 * c) : u32x4{0, 0, 0, 0};
+    for (int c = 0; c < DC; ++c) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qp + 16 * c);
+      qop[c] = q_ok ? v : u32x4{0, 0, 0, 0};
+    }
   }
 
-  f32x4 acc[DT];
+  f32x16 acc[DB];
 #pragma unroll
-  for (int t = 0; t < DT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY;  // running max of this lane's query (log2 domain)
+  for (int t = 0; t < DB; ++t) acc[t] = f32x16{};
+  // Reference max of this lane's query in the log2 domain; finite so that
+  // fully masked scores give exp2(-inf) = 0.
+  float m = -1e30f;
   float lsum = 0.f;     // partial sum over this lane's key slots
 
   const T* kg = reinterpret_cast<const T*>(a.k) + kvh * a.k_head;
@@ -163,208 +197,274 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
 
   u32x4 kreg[KLOADS];
   u32x4 vreg[VLOADS][4];
-  // Page ids of the keys this thread stages, fetched one tile ahead of the
-  // K/V loads so those never wait on a page-table read.
-  int32_t kpg[KLOADS];
-  int32_t vpg[VLOADS][4];
   auto split_pos = [&](int pos, int& page, int& off) {
-    if (a.bs_shift >= 0) {
-      page = pos >> a.bs_shift;
-      off = pos & (a.block_size - 1);
-    } else {
+    if constexpr (MODE == kDiv) {
       page = pos / a.block_size;
       off = pos - page * a.block_size;
+    } else {
+      page = pos >> a.bs_shift;
+      off = pos & (a.block_size - 1);
     }
   };
-  auto fetch_pages = [&](int t0) {
+  // Per-thread constant parts of the staged addresses (kGroup): K vector r is
+  // key kkey[r] of the tile, V unit keys are 4kq + j.
+  int kgrp[KLOADS], koff[KLOADS];
 #pragma unroll
-    for (int r = 0; r < KLOADS; ++r) {
-      const int key = (tid + 256 * r) / KCH;
-      const int pos = t0 + key;
-      int page, off;
-      split_pos(pos, page, off);
-      kpg[r] = pos < end ? table[page] : 0;
-    }
+  for (int r = 0; r < KLOADS; ++r) {
+    const int c = min(tid + kThreads * r, KVECS - 1);
+    const int key = c / KCH;
+    kgrp[r] = key >> 4;
+    koff[r] = (key & 15) * (int)a.k_token + (c % KCH) * 8;
+  }
+  int vgrp[VLOADS], voff[VLOADS][4];
 #pragma unroll
-    for (int r = 0; r < VLOADS; ++r) {
-      const int kq = (tid + 256 * r) / KCH;
+  for (int r = 0; r < VLOADS; ++r) {
+    const int u = min(tid + kThreads * r, VUNITS - 1);
+    const int kq = u % (kBN / 4), dc = u / (kBN / 4);
+    vgrp[r] = kq >> 2;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int pos = t0 + 4 * kq + j;
-        int page, off;
-        split_pos(pos, page, off);
-        vpg[r][j] = (tid + 256 * r < VUNITS && pos < end) ? table[page] : 0;
+    for (int j = 0; j < 4; ++j) voff[r][j] = (4 * (kq & 3) + j) * (int)a.v_token + dc * 8;
+  }
+  // Global -> registers for tile `t`. Keys past `end` never fault: the
+  // per-key modes re-read key end - 1; kGroup re-reads inside the last valid
+  // page (and zeroes V there), and whole groups past the end re-read the last
+  // valid group. Masked keys get P = 0.
+  auto fetch = [&](int t) {
+    const int t0 = t * kBN;
+    if constexpr (MODE == kGroup) {
+      constexpr int NG = kBN / 16;
+      int64_t gk[NG], gv[NG];
+      const int last_group = (end - 1) & ~15;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const int gpos = min(t0 + 16 * g, last_group);
+        const int64_t blk = table[gpos >> a.bs_shift];
+        const int64_t in_page = gpos & (a.block_size - 1);
+        gk[g] = blk * a.k_block + in_page * a.k_token;
+        gv[g] = blk * a.v_block + in_page * a.v_token;
       }
-    }
-  };
-  // Global -> registers for the tile starting at key t0 (zeros past `end`).
-  auto fetch = [&](int t0) {
+      auto pick = [](const int64_t (&v)[NG], int g) {
+        int64_t r = v[0];
 #pragma unroll
-    for (int r = 0; r < KLOADS; ++r) {
-      const int c = tid + 256 * r;
-      const int key = c / KCH, dc = c % KCH;
-      const int pos = t0 + key;
-      if (pos < end) {
-        int page, off;
-        split_pos(pos, page, off);
-        kreg[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-            kg + (int64_t)kpg[r] * a.k_block + off * a.k_token + dc * 8));
-      } else {
-        kreg[r] = u32x4{0, 0, 0, 0};
+        for (int i = 1; i < NG; ++i) r = g == i ? v[i] : r;
+        return r;
+      };
+#pragma unroll
+      for (int r = 0; r < KLOADS; ++r)
+        kreg[r] = load_cached(
+            reinterpret_cast<const u32x4*>(kg + pick(gk, kgrp[r]) + koff[r]));
+#pragma unroll
+      for (int r = 0; r < VLOADS; ++r) {
+        const T* base = vg + pick(gv, vgrp[r]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          vreg[r][j] = load_cached(reinterpret_cast<const u32x4*>(base + voff[r][j]));
       }
-    }
+      if (t0 + kBN > end) {  // edge tile: V past the end may be stale memory
 #pragma unroll
-    for (int r = 0; r < VLOADS; ++r) {
-      const int u = tid + 256 * r;
-      const int kq = u / KCH, dc = u % KCH;
+        for (int r = 0; r < VLOADS; ++r) {
+          const int kq = min(tid + kThreads * r, VUNITS - 1) % (kBN / 4);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int pos = t0 + 4 * kq + j;
-        if (u < VUNITS && pos < end) {
+          for (int j = 0; j < 4; ++j)
+            if (t0 + 4 * kq + j >= end) vreg[r][j] = u32x4{0, 0, 0, 0};
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < KLOADS; ++r) {
+        const int c = min(tid + kThreads * r, KVECS - 1);
+        int page, off;
+        split_pos(min(t0 + c / KCH, end - 1), page, off);
+        kreg[r] = load_cached(reinterpret_cast<const u32x4*>(
+            kg + (int64_t)table[page] * a.k_block + off * a.k_token + (c % KCH) * 8));
+      }
+#pragma unroll
+      for (int r = 0; r < VLOADS; ++r) {
+        const int u = min(tid + kThreads * r, VUNITS - 1);
+        const int kq = u % (kBN / 4), dc = u / (kBN / 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
           int page, off;
-          split_pos(pos, page, off);
-          vreg[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-              vg + (int64_t)vpg[r][j] * a.v_block + off * a.v_token + dc * 8));
-        } else {
-          vreg[r][j] = u32x4{0, 0, 0, 0};
+          split_pos(min(t0 + 4 * kq + j, end - 1), page, off);
+          vreg[r][j] = load_cached(reinterpret_cast<const u32x4*>(
+              vg + (int64_t)table[page] * a.v_block + off * a.v_token + dc * 8));
         }
       }
     }
   };
-  // Registers -> LDS: K row-major, V transposed to [d][key].
-  auto stash = [&]() {
+  // Registers -> LDS stage: K row-major, V transposed to [d][key]. V units are
+  // numbered key-quad fastest, so a wave's 8-byte writes of one dim row land on
+  // consecutive banks (2 passes per wave write, the minimum).
+  auto stash = [&](int stage) {
+    uint16_t* kd = ks[stage];
+    uint16_t* vd = vts[stage];
 #pragma unroll
     for (int r = 0; r < KLOADS; ++r) {
-      const int c = tid + 256 * r;
-      const int key = c / KCH, dc = c % KCH;
-      *reinterpret_cast<u32x4*>(&ks[key * Lds<D>::kPitch + dc * 8]) = kreg[r];
+      const int c = tid + kThreads * r;
+      if (KVECS % kThreads == 0 || c < KVECS)
+        *reinterpret_cast<u32x4*>(&kd[(c / KCH) * Lds<D>::kPitch + (c % KCH) * 8]) = kreg[r];
     }
 #pragma unroll
     for (int r = 0; r < VLOADS; ++r) {
-      const int u = tid + 256 * r;
+      const int u = tid + kThreads * r;
       if (u < VUNITS) {
-        const int kq = u / KCH, dc = u % KCH;
+        const int kq = u % (kBN / 4), dc = u / (kBN / 4);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {  // dim dc*8 + e, keys 4kq .. 4kq+3
-          const int w = e >> 1, sh = (e & 1) * 16;
-          const uint32_t k0 = (vreg[r][0][w] >> sh) & 0xffffu;
-          const uint32_t k1 = (vreg[r][1][w] >> sh) & 0xffffu;
-          const uint32_t k2 = (vreg[r][2][w] >> sh) & 0xffffu;
-          const uint32_t k3 = (vreg[r][3][w] >> sh) & 0xffffu;
-          *reinterpret_cast<u32x2*>(&vts[(dc * 8 + e) * Lds<D>::vPitch + 4 * kq]) =
-              u32x2{k0 | (k1 << 16), k2 | (k3 << 16)};
+          const int w = e >> 1;
+          // v_perm_b32: low or high 16-bit halves of two words -> one word.
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          const uint32_t k01 = __builtin_amdgcn_perm(vreg[r][1][w], vreg[r][0][w], sel);
+          const uint32_t k23 = __builtin_amdgcn_perm(vreg[r][3][w], vreg[r][2][w], sel);
+          *reinterpret_cast<u32x2*>(&vd[(dc * 8 + e) * Lds<D>::vPitch + 4 * kq]) =
+              u32x2{k01, k23};
         }
       }
     }
   };
 
-  if (end > 0) {
-    fetch_pages(0);
+  // Pipeline: tile t is consumed from LDS stage t % 2 while tile t + 1 sits in
+  // the other stage and tile t + 2 is in flight into registers. One barrier
+  // per tile separates "everyone finished tile t - 1" from overwriting its stage.
+  if (tiles > 0) {
     fetch(0);
-    if (kBN < end) fetch_pages(kBN);
+    stash(0);
+    if (tiles > 1) fetch(1);
   }
-  for (int t0 = 0; t0 < end; t0 += kBN) {
-    __syncthreads();  // previous tile fully consumed
-    stash();
+  for (int t = 0; t < tiles; ++t) {
+    const int stage = t & 1;
     __syncthreads();
-    if (t0 + kBN < end) {
-      fetch(t0 + kBN);  // in flight while we compute
-      if (t0 + 2 * kBN < end) fetch_pages(t0 + 2 * kBN);
+    if (t + 1 < tiles) {
+      stash(stage ^ 1);
+      if (t + 2 < tiles) fetch(t + 2);
     }
+    const uint16_t* kd = ks[stage];
+    const uint16_t* vd = vts[stage];
+    const int t0 = t * kBN;
 
-    // S^T tiles: st[kt] holds keys t0 + 16kt + 4grp + j for query `col`.
-    f32x4 st[kBN / 16];
+    // S^T blocks: st[kb] element j holds key 32kb + 8(j/4) + 4half + j%4.
+    f32x16 st[kBN / 32];
 #pragma unroll
-    for (int kt = 0; kt < kBN / 16; ++kt) {
-      f32x4 c4 = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < kBN / 32; ++kb) {
+      // All A-operand reads of the block first, then the MFMA chain.
+      u32x4 kop[DC];
 #pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        const u32x4 kop =
-            *reinterpret_cast<const u32x4*>(&ks[(16 * kt + col) * Lds<D>::kPitch + 32 * c + 8 * grp]);
-        c4 = Mfma<T>::run(kop, qop[c], c4);
-      }
-      st[kt] = c4;
+      for (int c = 0; c < DC; ++c)
+        kop[c] = *reinterpret_cast<const u32x4*>(
+            &kd[(32 * kb + col) * Lds<D>::kPitch + 16 * c + 8 * half]);
+      f32x16 c16 = f32x16{};
+#pragma unroll
+      for (int c = 0; c < DC; ++c) c16 = Mfma<T>::run(kop[c], qop[c], c16);
+      st[kb] = c16;
     }
-    // Scale, mask (causal + tile end), running max over the 4 lane groups.
+    // Causal mask (edge tiles only: tiles entirely below this wave's first
+    // query position and before `end` need none; wave-uniform test), then the
+    // raw running max over the lane pair (l, l ^ 32).
     float mx = -INFINITY;
+    if (t0 + kBN <= end && t0 + kBN - 1 <= wave_qpos0) {
 #pragma unroll
-    for (int kt = 0; kt < kBN / 16; ++kt) {
+      for (int kb = 0; kb < kBN / 32; ++kb)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int kpos = t0 + 16 * kt + 4 * grp + j;
-        const bool vis = q_ok && kpos < end && kpos <= qpos;
-        const float sv = vis ? st[kt][j] * a.scale_log2 : -INFINITY;
-        st[kt][j] = sv;
-        mx = fmaxf(mx, sv);
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[kb][j]);
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < kBN / 32; ++kb) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int kpos = t0 + 32 * kb + 8 * (j >> 2) + 4 * half + (j & 3);
+          const bool vis = q_ok && kpos < end && kpos <= qpos;
+          st[kb][j] = vis ? st[kb][j] : -INFINITY;
+          mx = fmaxf(mx, st[kb][j]);
+        }
       }
     }
-    mx = fmaxf(mx, shfl_xor_f32(mx, 16));
     mx = fmaxf(mx, shfl_xor_f32(mx, 32));
-    const float mnew = fmaxf(m, mx);
-    const float safe = mnew == -INFINITY ? 0.f : mnew;
-    const float corr = exp2f(m - safe);
-    lsum *= corr;
+    // Lazy rescaling (log2 domain, m finite from the start): the reference
+    // max only moves when some lane's max grows by more than 8, so P stays
+    // <= 2^8 and most tiles skip the O rescale.
+    const float mcand = mx * a.scale_log2;
+    if (__any(mcand > m + 8.f)) {
+      const float mnew = fmaxf(m, mcand);
+      const float corr = fast_exp2(m - mnew);
+      lsum *= corr;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) acc[t] *= corr;
-    // P^T operands per 32-key chunk: slots 0..3 from tile 2kc, 4..7 from 2kc+1.
-    u32x4 pop[kBN / 32];
+      for (int t2 = 0; t2 < DB; ++t2) acc[t2] *= corr;
+      m = mnew;
+    }
+    // P^T B-operands per 16-key chunk c: elements 8(c%2) .. +8 of st[c/2],
+    // i.e. keys 16c + 4half + {0..3} and 16c + 8 + 4half + {0..3}.
+    u32x4 pop[kBN / 16];
 #pragma unroll
-    for (int kc = 0; kc < kBN / 32; ++kc) {
+    for (int c = 0; c < kBN / 16; ++c) {
       float p[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        p[j] = exp2f(st[2 * kc][j] - safe);
-        p[4 + j] = exp2f(st[2 * kc + 1][j] - safe);
+      for (int i = 0; i < 8; ++i) {
+        p[i] = fast_exp2(fmaf(st[c >> 1][8 * (c & 1) + i], a.scale_log2, -m));
+        lsum += p[i];
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) lsum += p[j];
-      pop[kc] = u32x4{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
-                      pack2<T>(p[6], p[7])};
+      pop[c] = u32x4{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
+                     pack2<T>(p[6], p[7])};
     }
-    m = mnew;
-    // O^T[d, q] += V^T[d, keys] P^T[keys, q]
+    // O^T[d, q] += V^T[d, keys] P^T[keys, q], A-operand keys matching pop's.
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      const uint16_t* vrow = &vts[(16 * t + col) * Lds<D>::vPitch];
+    for (int db = 0; db < DB; ++db) {
+      const uint16_t* vrow = &vd[(32 * db + col) * Lds<D>::vPitch];
+      u32x4 vop[kBN / 16];
 #pragma unroll
-      for (int kc = 0; kc < kBN / 32; ++kc) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + 32 * kc + 4 * grp);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 32 * kc + 16 + 4 * grp);
-        acc[t] = Mfma<T>::run(u32x4{lo[0], lo[1], hi[0], hi[1]}, pop[kc], acc[t]);
+      for (int c = 0; c < kBN / 16; ++c) {
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + 16 * c + 4 * half);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16 * c + 8 + 4 * half);
+        vop[c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
+#pragma unroll
+      for (int c = 0; c < kBN / 16; ++c) acc[db] = Mfma<T>::run(vop[c], pop[c], acc[db]);
     }
   }
 
-  lsum += shfl_xor_f32(lsum, 16);
   lsum += shfl_xor_f32(lsum, 32);
   if (!q_ok) return;
-  const float inv = 1.f / fmaxf(lsum, 1e-30f);
+  const float inv = fast_rcp(fmaxf(lsum, 1e-30f));
   T* op = reinterpret_cast<T*>(a.out) + (int64_t)(q_begin + qi) * a.o_token + head * a.o_head;
 #pragma unroll
-  for (int t = 0; t < DT; ++t) {
-    const int d = 16 * t + 4 * grp;
-    *reinterpret_cast<u32x2*>(op + d) =
-        u32x2{pack2<T>(acc[t][0] * inv, acc[t][1] * inv), pack2<T>(acc[t][2] * inv, acc[t][3] * inv)};
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {  // rows 32db + 8g + 4half + {0..3}
+      const int d = 32 * db + 8 * g + 4 * half;
+      *reinterpret_cast<u32x2*>(op + d) =
+          u32x2{pack2<T>(acc[db][4 * g] * inv, acc[db][4 * g + 1] * inv),
+                pack2<T>(acc[db][4 * g + 2] * inv, acc[db][4 * g + 3] * inv)};
+    }
   }
 }
 
-template <typename T>
-bool launch_prefill(int d, dim3 grid, hipStream_t s, const PrefillArgs& a) {
+template <typename T, int MODE>
+bool launch_prefill_d(int d, dim3 grid, hipStream_t s, const PrefillArgs& a) {
   switch (d) {
-#define VRH_D(DV)                                                                    \
-  case DV:                                                                           \
-    hipLaunchKernelGGL((paged_prefill_kernel<T, DV>), grid, dim3(256), 0, s, a); \
+#define VRH_D(DV)                                                                          \
+  case DV:                                                                                 \
+    hipLaunchKernelGGL((paged_prefill_kernel<T, DV, MODE>), grid, dim3(kThreads), 0, s, a); \
     return true;
     VRH_D(32)
     VRH_D(64)
     VRH_D(96)
     VRH_D(128)
+#if VRH_PREFILL_BN <= 64
     VRH_D(160)
     VRH_D(192)
     VRH_D(224)
+#endif
 #undef VRH_D
     default: return false;
   }
+}
+
+template <typename T>
+bool launch_prefill(int d, dim3 grid, hipStream_t s, const PrefillArgs& a) {
+  // kGroup keeps per-thread offsets (< 16 tokens) in 32 bits.
+  const bool small_strides = a.k_token < (1 << 26) && a.v_token < (1 << 26);
+  if (a.bs_shift >= 4 && small_strides) return launch_prefill_d<T, kGroup>(d, grid, s, a);
+  if (a.bs_shift >= 0) return launch_prefill_d<T, kShift>(d, grid, s, a);
+  return launch_prefill_d<T, kDiv>(d, grid, s, a);
 }
 
 }  // namespace
@@ -448,15 +548,16 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   a.table_width = table_width;
   a.skip_q = route_decode ? kDecodeQ : 0;
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
-  const unsigned qblocks = (unsigned)ceil_div(max_seqlen_q, kBM);
-  for (int64_t first = 0; first < num_seqs; first += 65535) {
-    a.seq_base = first;
-    const unsigned count = (unsigned)std::min<int64_t>(num_seqs - first, 65535);
-    dim3 grid(qblocks, (unsigned)q_heads, count);
-    const bool ok = dtype == VRH_DTYPE_BF16 ? launch_prefill<bf16_t>(head_dim, grid, s, a)
-                                            : launch_prefill<f16_t>(head_dim, grid, s, a);
-    VRH_CHECK_ARG(ok, "vrh_paged_prefill: no kernel for head_dim %d", head_dim);
-  }
+  a.num_seqs = num_seqs;
+  a.kv_heads = kv_heads;
+  a.qblocks = ceil_div(max_seqlen_q, kBM);
+  const int64_t groups = num_seqs * kv_heads;
+  const int64_t launched = (groups + 7) / 8 * 8 * (int64_t)a.group * a.qblocks;
+  VRH_CHECK_ARG(launched < (1ll << 31), "vrh_paged_prefill: too many work items");
+  const bool ok = dtype == VRH_DTYPE_BF16
+                      ? launch_prefill<bf16_t>(head_dim, dim3((unsigned)launched), s, a)
+                      : launch_prefill<f16_t>(head_dim, dim3((unsigned)launched), s, a);
+  VRH_CHECK_ARG(ok, "vrh_paged_prefill: no kernel for head_dim %d", head_dim);
   if (route_decode) {
     // Decode rows of the packed batch: split-KV single-query kernel.
     const int rc = vrh_decode_rows(
