@@ -53,6 +53,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kWQ = 32;                    // queries per wave
 constexpr int kBM = kWQ * kWaves;          // queries per workgroup
 constexpr int kBN = VRH_PREFILL_BN;        // keys per tile
+constexpr int kTableSeg = 512;             // page ids staged in LDS at a time
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
@@ -105,6 +106,13 @@ struct PrefillArgs {
 
 // LDS tiles, two stages each. Row pitches (elements) are padded by 16 bytes so
 // the 32 rows an MFMA operand read touches spread over the banks.
+// V^T tile column swizzle: the 4-key group g of dim row d is stored at group
+// position g ^ (4 * ((d >> 4) & 3)). A wave's transposed 8-byte writes (16
+// dim chunks x 4 key quads per instruction) then hit every bank exactly twice.
+__device__ __forceinline__ int vt_group(int d, int g) {
+  return (g ^ (((d >> 4) & 3) << 2)) & (kBN / 4 - 1);
+}
+
 template <int D>
 struct Lds {
   static constexpr int kPitch = D + 8;    // K tile [kBN][kPitch]
@@ -117,10 +125,8 @@ struct Lds {
 #define VRH_PREFILL_WG_PER_CU 2
 #endif
 
-// Page addressing modes: kDiv (any block size), kShift (power of two), kGroup
-// (power of two >= 16: a 16-key group never straddles a page, so the four
-// group base addresses of a tile are wave-uniform scalars).
-enum PageMode { kDiv = 0, kShift = 1, kGroup = 2 };
+// Page addressing modes: kDiv (any block size), kShift (power of two).
+enum PageMode { kDiv = 0, kShift = 1 };
 
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill_kernel(PrefillArgs a) {
@@ -195,232 +201,195 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
   const T* kg = reinterpret_cast<const T*>(a.k) + kvh * a.k_head;
   const T* vg = reinterpret_cast<const T*>(a.v) + kvh * a.v_head;
 
-  u32x4 kreg[KLOADS];
-  u32x4 vreg[VLOADS][4];
-  auto split_pos = [&](int pos, int& page, int& off) {
-    if constexpr (MODE == kDiv) {
-      page = pos / a.block_size;
-      off = pos - page * a.block_size;
-    } else {
-      page = pos >> a.bs_shift;
-      off = pos & (a.block_size - 1);
-    }
+  // One tile of staged K/V in registers.
+  struct Regs {
+    u32x4 k[KLOADS];
+    u32x4 v[VLOADS][4];
   };
-  // Per-thread constant parts of the staged addresses (kGroup): K vector r is
-  // key kkey[r] of the tile, V unit keys are 4kq + j.
-  int kgrp[KLOADS], koff[KLOADS];
-#pragma unroll
-  for (int r = 0; r < KLOADS; ++r) {
-    const int c = min(tid + kThreads * r, KVECS - 1);
-    const int key = c / KCH;
-    kgrp[r] = key >> 4;
-    koff[r] = (key & 15) * (int)a.k_token + (c % KCH) * 8;
-  }
-  int vgrp[VLOADS], voff[VLOADS][4];
-#pragma unroll
-  for (int r = 0; r < VLOADS; ++r) {
-    const int u = min(tid + kThreads * r, VUNITS - 1);
-    const int kq = u % (kBN / 4), dc = u / (kBN / 4);
-    vgrp[r] = kq >> 2;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) voff[r][j] = (4 * (kq & 3) + j) * (int)a.v_token + dc * 8;
-  }
-  // Global -> registers for tile `t`. Keys past `end` never fault: the
-  // per-key modes re-read key end - 1; kGroup re-reads inside the last valid
-  // page (and zeroes V there), and whole groups past the end re-read the last
-  // valid group. Masked keys get P = 0.
-  auto fetch = [&](int t) {
+  // A 512-entry segment of the page table is staged in LDS. A page id
+  // fetched with a vector load would make every later K/V load wait for all
+  // earlier ones (vmcnt retires in order), so the per-key lookups read LDS;
+  // the segment is refilled (all waves, between barriers) when a tile's pages
+  // run past it.
+  __shared__ int32_t tbl_lds[kTableSeg];
+  int tbl_base = 0;
+  auto load_table = [&](int base) {
+    __syncthreads();
+    for (int i = tid; i < kTableSeg; i += kThreads)
+      tbl_lds[i] = base + i < a.table_width ? table[base + i] : 0;
+    __syncthreads();
+    tbl_base = base;
+  };
+  auto page_of = [&](int pos) {
+    if constexpr (MODE == kDiv) return pos / a.block_size;
+    else return pos >> a.bs_shift;
+  };
+  load_table(0);
+  // Global -> registers for tile `t`. Branch-free: keys past `end` re-read key
+  // end - 1 (real data); the softmax masks them, so P is 0 there.
+  auto fetch = [&](int t, Regs& R) {
     const int t0 = t * kBN;
-    if constexpr (MODE == kGroup) {
-      constexpr int NG = kBN / 16;
-      int64_t gk[NG], gv[NG];
-      const int last_group = (end - 1) & ~15;
+    {
+      const int last_page = page_of(min(t0 + kBN, end) - 1);
+      if (last_page >= tbl_base + kTableSeg) load_table(page_of(t0));
+    }
+    auto slot = [&](int pos, int64_t block_stride, int64_t token_stride) {
+      const int pg = page_of(pos);
+      const int off = pos - pg * a.block_size;
+      return (int64_t)tbl_lds[pg - tbl_base] * block_stride + (int64_t)off * token_stride;
+    };
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const int gpos = min(t0 + 16 * g, last_group);
-        const int64_t blk = table[gpos >> a.bs_shift];
-        const int64_t in_page = gpos & (a.block_size - 1);
-        gk[g] = blk * a.k_block + in_page * a.k_token;
-        gv[g] = blk * a.v_block + in_page * a.v_token;
-      }
-      auto pick = [](const int64_t (&v)[NG], int g) {
-        int64_t r = v[0];
+    for (int r = 0; r < KLOADS; ++r) {
+      const int c = min(tid + kThreads * r, KVECS - 1);
+      const int pos = min(t0 + c / KCH, end - 1);
+      R.k[r] = load_cached(
+          reinterpret_cast<const u32x4*>(kg + slot(pos, a.k_block, a.k_token) + (c % KCH) * 8));
+    }
 #pragma unroll
-        for (int i = 1; i < NG; ++i) r = g == i ? v[i] : r;
-        return r;
-      };
+    for (int r = 0; r < VLOADS; ++r) {
+      const int u = min(tid + kThreads * r, VUNITS - 1);
+      const int kq = u / KCH, dc = u % KCH;
 #pragma unroll
-      for (int r = 0; r < KLOADS; ++r)
-        kreg[r] = load_cached(
-            reinterpret_cast<const u32x4*>(kg + pick(gk, kgrp[r]) + koff[r]));
-#pragma unroll
-      for (int r = 0; r < VLOADS; ++r) {
-        const T* base = vg + pick(gv, vgrp[r]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          vreg[r][j] = load_cached(reinterpret_cast<const u32x4*>(base + voff[r][j]));
-      }
-      if (t0 + kBN > end) {  // edge tile: V past the end may be stale memory
-#pragma unroll
-        for (int r = 0; r < VLOADS; ++r) {
-          const int kq = min(tid + kThreads * r, VUNITS - 1) % (kBN / 4);
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (t0 + 4 * kq + j >= end) vreg[r][j] = u32x4{0, 0, 0, 0};
-        }
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < KLOADS; ++r) {
-        const int c = min(tid + kThreads * r, KVECS - 1);
-        int page, off;
-        split_pos(min(t0 + c / KCH, end - 1), page, off);
-        kreg[r] = load_cached(reinterpret_cast<const u32x4*>(
-            kg + (int64_t)table[page] * a.k_block + off * a.k_token + (c % KCH) * 8));
-      }
-#pragma unroll
-      for (int r = 0; r < VLOADS; ++r) {
-        const int u = min(tid + kThreads * r, VUNITS - 1);
-        const int kq = u % (kBN / 4), dc = u / (kBN / 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          int page, off;
-          split_pos(min(t0 + 4 * kq + j, end - 1), page, off);
-          vreg[r][j] = load_cached(reinterpret_cast<const u32x4*>(
-              vg + (int64_t)table[page] * a.v_block + off * a.v_token + dc * 8));
-        }
+      for (int j = 0; j < 4; ++j) {
+        const int pos = min(t0 + 4 * kq + j, end - 1);
+        R.v[r][j] = load_cached(
+            reinterpret_cast<const u32x4*>(vg + slot(pos, a.v_block, a.v_token) + dc * 8));
       }
     }
   };
-  // Registers -> LDS stage: K row-major, V transposed to [d][key]. V units are
-  // numbered key-quad fastest, so a wave's 8-byte writes of one dim row land on
-  // consecutive banks (2 passes per wave write, the minimum).
-  auto stash = [&](int stage) {
+  // Registers -> LDS stage: K row-major, V transposed to [d][key] with the
+  // column swizzle of vt_group (2 passes per wave write, the minimum).
+  auto stash = [&](int stage, const Regs& R) {
     uint16_t* kd = ks[stage];
     uint16_t* vd = vts[stage];
 #pragma unroll
     for (int r = 0; r < KLOADS; ++r) {
       const int c = tid + kThreads * r;
       if (KVECS % kThreads == 0 || c < KVECS)
-        *reinterpret_cast<u32x4*>(&kd[(c / KCH) * Lds<D>::kPitch + (c % KCH) * 8]) = kreg[r];
+        *reinterpret_cast<u32x4*>(&kd[(c / KCH) * Lds<D>::kPitch + (c % KCH) * 8]) = R.k[r];
     }
 #pragma unroll
     for (int r = 0; r < VLOADS; ++r) {
       const int u = tid + kThreads * r;
       if (u < VUNITS) {
-        const int kq = u % (kBN / 4), dc = u / (kBN / 4);
+        const int kq = u / KCH, dc = u % KCH;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {  // dim dc*8 + e, keys 4kq .. 4kq+3
           const int w = e >> 1;
           // v_perm_b32: low or high 16-bit halves of two words -> one word.
           const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-          const uint32_t k01 = __builtin_amdgcn_perm(vreg[r][1][w], vreg[r][0][w], sel);
-          const uint32_t k23 = __builtin_amdgcn_perm(vreg[r][3][w], vreg[r][2][w], sel);
-          *reinterpret_cast<u32x2*>(&vd[(dc * 8 + e) * Lds<D>::vPitch + 4 * kq]) =
+          const uint32_t k01 = __builtin_amdgcn_perm(R.v[r][1][w], R.v[r][0][w], sel);
+          const uint32_t k23 = __builtin_amdgcn_perm(R.v[r][3][w], R.v[r][2][w], sel);
+          const int d = dc * 8 + e;
+          *reinterpret_cast<u32x2*>(&vd[d * Lds<D>::vPitch + 4 * vt_group(d, kq)]) =
               u32x2{k01, k23};
         }
       }
     }
   };
 
-  // Pipeline: tile t is consumed from LDS stage t % 2 while tile t + 1 sits in
-  // the other stage and tile t + 2 is in flight into registers. One barrier
-  // per tile separates "everyone finished tile t - 1" from overwriting its stage.
-  if (tiles > 0) {
-    fetch(0);
-    stash(0);
-    if (tiles > 1) fetch(1);
-  }
-  for (int t = 0; t < tiles; ++t) {
+  // One 64-key LDS tile is consumed as 32-key sub-blocks, each a full online
+  // softmax step: only one S^T accumulator and two P^T operands are live.
+  auto compute = [&](int t) {
     const int stage = t & 1;
-    __syncthreads();
-    if (t + 1 < tiles) {
-      stash(stage ^ 1);
-      if (t + 2 < tiles) fetch(t + 2);
-    }
     const uint16_t* kd = ks[stage];
     const uint16_t* vd = vts[stage];
-    const int t0 = t * kBN;
-
-    // S^T blocks: st[kb] element j holds key 32kb + 8(j/4) + 4half + j%4.
-    f32x16 st[kBN / 32];
 #pragma unroll
     for (int kb = 0; kb < kBN / 32; ++kb) {
-      // All A-operand reads of the block first, then the MFMA chain.
-      u32x4 kop[DC];
+      const int k0 = t * kBN + 32 * kb;  // first key of the sub-block
+      // S^T: element j holds key k0 + 8(j/4) + 4half + j%4 for query `col`.
+      f32x16 st = f32x16{};
 #pragma unroll
-      for (int c = 0; c < DC; ++c)
-        kop[c] = *reinterpret_cast<const u32x4*>(
-            &kd[(32 * kb + col) * Lds<D>::kPitch + 16 * c + 8 * half]);
-      f32x16 c16 = f32x16{};
+      for (int c0 = 0; c0 < DC; c0 += 4) {
+        u32x4 kop[4];  // A-operand reads in groups of 4, then their MFMAs
 #pragma unroll
-      for (int c = 0; c < DC; ++c) c16 = Mfma<T>::run(kop[c], qop[c], c16);
-      st[kb] = c16;
-    }
-    // Causal mask (edge tiles only: tiles entirely below this wave's first
-    // query position and before `end` need none; wave-uniform test), then the
-    // raw running max over the lane pair (l, l ^ 32).
-    float mx = -INFINITY;
-    if (t0 + kBN <= end && t0 + kBN - 1 <= wave_qpos0) {
+        for (int c = 0; c < 4 && c0 + c < DC; ++c)
+          kop[c] = *reinterpret_cast<const u32x4*>(
+              &kd[(32 * kb + col) * Lds<D>::kPitch + 16 * (c0 + c) + 8 * half]);
 #pragma unroll
-      for (int kb = 0; kb < kBN / 32; ++kb)
+        for (int c = 0; c < 4 && c0 + c < DC; ++c) st = Mfma<T>::run(kop[c], qop[c0 + c], st);
+      }
+      // Causal mask only where needed (wave-uniform test: sub-blocks entirely
+      // below this wave's first query position and before `end` need none),
+      // then the raw running max over the lane pair (l, l ^ 32).
+      float mx = -INFINITY;
+      if (k0 + 32 <= end && k0 + 31 <= wave_qpos0) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[kb][j]);
-    } else {
-#pragma unroll
-      for (int kb = 0; kb < kBN / 32; ++kb) {
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[j]);
+      } else {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          const int kpos = t0 + 32 * kb + 8 * (j >> 2) + 4 * half + (j & 3);
+          const int kpos = k0 + 8 * (j >> 2) + 4 * half + (j & 3);
           const bool vis = q_ok && kpos < end && kpos <= qpos;
-          st[kb][j] = vis ? st[kb][j] : -INFINITY;
-          mx = fmaxf(mx, st[kb][j]);
+          st[j] = vis ? st[j] : -INFINITY;
+          mx = fmaxf(mx, st[j]);
         }
       }
-    }
-    mx = fmaxf(mx, shfl_xor_f32(mx, 32));
-    // Lazy rescaling (log2 domain, m finite from the start): the reference
-    // max only moves when some lane's max grows by more than 8, so P stays
-    // <= 2^8 and most tiles skip the O rescale.
-    const float mcand = mx * a.scale_log2;
-    if (__any(mcand > m + 8.f)) {
-      const float mnew = fmaxf(m, mcand);
-      const float corr = fast_exp2(m - mnew);
-      lsum *= corr;
+      mx = fmaxf(mx, shfl_xor_f32(mx, 32));
+      // Lazy rescaling (log2 domain, m finite from the start): the reference
+      // max only moves when some lane's max grows by more than 8, so P stays
+      // <= 2^8 and most sub-blocks skip the O rescale.
+      const float mcand = mx * a.scale_log2;
+      if (__any(mcand > m + 8.f)) {
+        const float mnew = fmaxf(m, mcand);
+        const float corr = fast_exp2(m - mnew);
+        lsum *= corr;
 #pragma unroll
-      for (int t2 = 0; t2 < DB; ++t2) acc[t2] *= corr;
-      m = mnew;
-    }
-    // P^T B-operands per 16-key chunk c: elements 8(c%2) .. +8 of st[c/2],
-    // i.e. keys 16c + 4half + {0..3} and 16c + 8 + 4half + {0..3}.
-    u32x4 pop[kBN / 16];
-#pragma unroll
-    for (int c = 0; c < kBN / 16; ++c) {
-      float p[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        p[i] = fast_exp2(fmaf(st[c >> 1][8 * (c & 1) + i], a.scale_log2, -m));
-        lsum += p[i];
+        for (int t2 = 0; t2 < DB; ++t2) acc[t2] *= corr;
+        m = mnew;
       }
-      pop[c] = u32x4{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
-                     pack2<T>(p[6], p[7])};
-    }
-    // O^T[d, q] += V^T[d, keys] P^T[keys, q], A-operand keys matching pop's.
+      // P^T B-operands per 16-key chunk c: elements 8c .. 8c+7 of st, i.e.
+      // keys k0 + 16c + 4half + {0..3} and k0 + 16c + 8 + 4half + {0..3}.
+      u32x4 pop[2];
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const uint16_t* vrow = &vd[(32 * db + col) * Lds<D>::vPitch];
-      u32x4 vop[kBN / 16];
+      for (int c = 0; c < 2; ++c) {
+        float p[8];
 #pragma unroll
-      for (int c = 0; c < kBN / 16; ++c) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + 16 * c + 4 * half);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16 * c + 8 + 4 * half);
-        vop[c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        for (int i = 0; i < 8; ++i) {
+          p[i] = fast_exp2(fmaf(st[8 * c + i], a.scale_log2, -m));
+          lsum += p[i];
+        }
+        pop[c] = u32x4{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
+                       pack2<T>(p[6], p[7])};
       }
+      // O^T[d, q] += V^T[d, keys] P^T[keys, q], A-operand keys matching pop's.
 #pragma unroll
-      for (int c = 0; c < kBN / 16; ++c) acc[db] = Mfma<T>::run(vop[c], pop[c], acc[db]);
+      for (int db = 0; db < DB; ++db) {
+        const int d = 32 * db + col;
+        const uint16_t* vrow = &vd[d * Lds<D>::vPitch];
+        u32x4 vop[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {  // key groups 8kb + 4c + half and + 2
+          const int g = 8 * kb + 4 * c + half;
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + 4 * vt_group(d, g));
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 4 * vt_group(d, g + 2));
+          vop[c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[db] = Mfma<T>::run(vop[c], pop[c], acc[db]);
+      }
     }
-  }
+  };
 
+
+  // Pipeline: tile t is consumed from LDS stage t % 2 while tile t + 1 sits
+  // in the other stage and tile t + 2 is in flight into registers. One
+  // barrier per tile separates "everyone finished tile t - 1" from
+  // overwriting its stage.
+  Regs ra;
+  if (tiles > 0) {
+    fetch(0, ra);
+    stash(0, ra);
+    if (tiles > 1) fetch(1, ra);
+  }
+  for (int t = 0; t < tiles; ++t) {
+    __syncthreads();
+    if (t + 1 < tiles) {
+      stash((t & 1) ^ 1, ra);
+      if (t + 2 < tiles) fetch(t + 2, ra);
+    }
+    compute(t);
+  }
   lsum += shfl_xor_f32(lsum, 32);
   if (!q_ok) return;
   const float inv = fast_rcp(fmaxf(lsum, 1e-30f));
@@ -460,9 +429,6 @@ bool launch_prefill_d(int d, dim3 grid, hipStream_t s, const PrefillArgs& a) {
 
 template <typename T>
 bool launch_prefill(int d, dim3 grid, hipStream_t s, const PrefillArgs& a) {
-  // kGroup keeps per-thread offsets (< 16 tokens) in 32 bits.
-  const bool small_strides = a.k_token < (1 << 26) && a.v_token < (1 << 26);
-  if (a.bs_shift >= 4 && small_strides) return launch_prefill_d<T, kGroup>(d, grid, s, a);
   if (a.bs_shift >= 0) return launch_prefill_d<T, kShift>(d, grid, s, a);
   return launch_prefill_d<T, kDiv>(d, grid, s, a);
 }
