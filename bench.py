@@ -8,10 +8,12 @@ over that layer's view of the pool (inputs resident in HBM).
 
 value = algorithmic decode bytes per step / wall time per step, in GB/s
 (K+V of every visible token per row + q/out + page-table entries).
-Also reported (same JSON line): KV-append GB/s for a 24-layer batched append
-of the step's tokens and for the config-4 chunk append (8,240 rows), packed
-prefill TFLOP/s at config 4, the HIP-event roofline of the decode kernel pair,
-and the CPU oracle baseline on a bounded row sample.
+Also reported (same JSON line, "extras"): KV-append GB/s for a 24-layer
+batched append of the step's tokens and for the config-4 chunk append (8,039
+rows), whole-block copy and LAST_EXITED finalize GB/s on the config-2 pool,
+config-3 (SHARED, shared prefix pages) decode GB/s, packed prefill TFLOP/s at
+config 4; plus the HIP-event roofline of the decode kernel pair and the CPU
+oracle baseline on a bounded sample.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3]
 """
@@ -92,20 +94,24 @@ def event_time_ms(fn, repeats):
     return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / repeats
 
 
-def graph_time_ms(fn, replays):
-    """Kernel time of ``fn`` without Python launch overhead: capture it once in
-    a HIP graph and time ``replays`` back-to-back replays with HIP events."""
+def graph_time_ms(fns, replays=10):
+    """Kernel time per call without Python launch overhead: capture the calls
+    ``fns`` (one or a list, run back to back) in one HIP graph, replay it
+    ``replays`` times and divide the HIP-event time by the number of calls."""
     import torch
 
+    fns = fns if isinstance(fns, (list, tuple)) else [fns]
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
-        fn()  # warm up outside capture (library load, allocator)
+        for fn in fns:
+            fn()  # warm up outside capture (library load, allocator)
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        fn()
+        for fn in fns:
+            fn()
     graph.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
@@ -115,7 +121,7 @@ def graph_time_ms(fn, replays):
         graph.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / replays
+    return start.elapsed_time(end) / (replays * len(fns))
 
 
 def cpu_baseline(work, budget_s):
@@ -174,6 +180,8 @@ def main():
     from vllm_rlt.kernels.hip_attention import (
         kv_append,
         kv_append_layers,
+        kv_copy_blocks,
+        kv_finalize,
         paged_attention,
         paged_prefill_attention,
     )
@@ -251,24 +259,69 @@ def main():
     if not args.skip_extras:
         # 24-layer batched append of the step's 64 tokens (one launch).
         append_layers_ms = graph_time_ms(
-            lambda: kv_append_layers(work.key_cache, work.value_cache, 0, work.k_new, work.v_new,
-                                     work.write_blocks, work.write_offsets), 100)
+            [lambda: kv_append_layers(work.key_cache, work.value_cache, 0, work.k_new, work.v_new,
+                                      work.write_blocks, work.write_offsets)] * 32)
         append_layers_bytes = work.append_bytes(layers)
         # single-layer decode append (latency)
         single_ms = graph_time_ms(
-            lambda: kv_append(kviews[0], vviews[0], work.k_new[0], work.v_new[0],
-                              work.write_blocks, work.write_offsets), 100)
+            [lambda layer=layer: kv_append(kviews[layer], vviews[layer], work.k_new[layer],
+                                           work.v_new[layer], work.write_blocks,
+                                           work.write_offsets) for layer in range(layers)])
         extras = {"append_24_layers": {
             "gbs": round(append_layers_bytes / (append_layers_ms * 1e-3) / 1e9, 2),
             "us": round(append_layers_ms * 1e3, 2), "bytes": append_layers_bytes},
-            "append_one_layer_us": round(single_ms * 1e3, 2)}
+            "append_one_layer_us": round(single_ms * 1e3, 2),
+                  "append_one_layer_gbs": round(work.append_bytes(1) / (single_ms * 1e-3) / 1e9, 2)}
+        # Whole-block copy (copy-on-write / compaction): 64 random 3 MiB blocks
+        # per call, a different set each call (no cache can serve the repeats).
+        gen = torch.Generator().manual_seed(5)
+        perm = torch.randperm(work.num_blocks, generator=gen)[: 128 * 16].to(device).view(16, 128)
+        copy_ms = graph_time_ms(
+            [lambda i=i: kv_copy_blocks(work.key_cache, work.value_cache, perm[i, :64],
+                                        perm[i, 64:]) for i in range(16)], replays=2)
+        block_bytes = work.key_cache[0].numel() * work.key_cache.element_size()
+        copy_bytes = 64 * block_bytes * 2 * 2
+        extras["copy_blocks_64x3MiB"] = {
+            "gbs": round(copy_bytes / (copy_ms * 1e-3) / 1e9, 2), "us": round(copy_ms * 1e3, 2)}
+        # LAST_EXITED finalize of the step's 64 tokens from their depth into
+        # every deeper plane, all 24 layers (device descriptors).
+        depths = work.extra["depths"]
+        planes = 4
+        plane_tables = work.extra["plane_tables"]
+        width = max(len(t) for t in plane_tables)
+        table_dev = torch.zeros((len(plane_tables), width), dtype=torch.int32)
+        for i, pages in enumerate(plane_tables):
+            table_dev[i, : len(pages)] = torch.tensor(pages, dtype=torch.int32)
+        table_dev = table_dev.to(device)
+        positions = (work.context_lengths - 1).to(torch.int64).cpu()
+        desc = torch.stack([torch.arange(work.rows), depths.to(torch.int64), positions], 1).to(device)
+        fin_ms = graph_time_ms(
+            [lambda: kv_finalize(work.key_cache, work.value_cache, desc, table_dev, planes)] * 32)
+        slot = work.key_cache.shape[3] * work.key_cache.shape[4] * work.key_cache.element_size()
+        fin_bytes = int((planes - 1 - depths).sum()) * layers * slot * 2 * 2
+        extras["finalize_64_tokens_24_layers"] = {
+            "gbs": round(fin_bytes / (fin_ms * 1e-3) / 1e9, 2), "us": round(fin_ms * 1e3, 2),
+            "bytes": fin_bytes}
         result["cpu_baseline"] = cpu_baseline(work, args.cpu_seconds)
         del work, kviews, vviews
+        torch.cuda.empty_cache()
+        # config 3: SHARED layout, 16 groups x 8 requests sharing 64 prefix pages.
+        w3 = workloads.config3(device=device)
+        k3, v3 = w3.key_cache[:, 0], w3.value_cache[:, 0]
+        dec3_ms = event_time_ms(
+            lambda: paged_attention(w3.q, k3, v3, w3.block_tables, w3.context_lengths), 20)
+        es = w3.key_cache.element_size()
+        unique = w3.extra["unique_tokens"] * 2 * w3.key_cache.shape[3] * w3.key_cache.shape[4] * es
+        extras["decode_config3_shared_prefix"] = {
+            "gbs_per_row_bytes": round(w3.decode_bytes() / (dec3_ms * 1e-3) / 1e9, 2),
+            "gbs_unique_bytes": round(unique / (dec3_ms * 1e-3) / 1e9, 2),
+            "us": round(dec3_ms * 1e3, 2), "rows": w3.rows}
+        del w3, k3, v3
         torch.cuda.empty_cache()
         pw = workloads.config4(device=device)
         kc, vc = pw.key_cache[:, 0], pw.value_cache[:, 0]
         append_ms = graph_time_ms(
-            lambda: kv_append(kc, vc, pw.k_new, pw.v_new, pw.write_blocks, pw.write_offsets), 100)
+            [lambda: kv_append(kc, vc, pw.k_new, pw.v_new, pw.write_blocks, pw.write_offsets)] * 32)
         prefill_ms = event_time_ms(
             lambda: paged_prefill_attention(pw.q, kc, vc, pw.block_tables, pw.context_lengths,
                                             pw.cu_seqlens_q, pw.max_seqlen_q), 10)
