@@ -16,9 +16,9 @@
 //    Output lane l holds query l % 32 and keys 8 * (j / 4) + 4 * (l / 32) + j % 4.
 //  * O^T = V^T P^T: the S^T accumulator of a lane is already a P^T B-operand
 //    (same query column, keys in the lane's k-slots), so P never goes through
-//    LDS. V is stored transposed in LDS ([d][key]) when the tile is staged; A
-//    reads are two 8-byte reads whose keys match the P^T k-slots. Only the
-//    pairing of A and B k-slots matters, not the hardware's k order.
+//    LDS. V stays row-major in LDS; the V^T A-operand comes from two
+//    ds_read_b64_tr_b16 transposed reads whose keys match the P^T k-slots.
+//    Only the pairing of A and B k-slots matters, not the hardware's k order.
 //  * Per-query running max is reduced over the lane pair (l, l ^ 32) each
 //    tile; the running sum stays a per-lane partial until the end.
 // Other dtypes / head dims (f32 reference checks, odd dims) run the decode
@@ -104,22 +104,31 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-// LDS tiles, two stages each. Row pitches (elements) are padded by 16 bytes so
-// the 32 rows an MFMA operand read touches spread over the banks.
-// V^T tile column swizzle: the 4-key group g of dim row d is stored at group
-// position g ^ (4 * ((d >> 4) & 3)). A wave's transposed 8-byte writes (16
-// dim chunks x 4 key quads per instruction) then hit every bank exactly twice.
-__device__ __forceinline__ int vt_group(int d, int g) {
-  return (g ^ (((d >> 4) & 3) << 2)) & (kBN / 4 - 1);
-}
-
+// LDS tiles, two stages each, both row-major [key][d].
+//  * K rows are padded by 16 bytes so the 32 rows an MFMA operand read touches
+//    spread over the banks.
+//  * V is read with ds_read_b64_tr_b16, which hands each lane of a 16-lane
+//    group one dim of four consecutive keys (the transposed operand). One
+//    wave read covers 8 rows x 64 contiguous bytes; a row pitch of 16 or 48
+//    words mod 64 puts those 8 row segments on distinct banks.
 template <int D>
 struct Lds {
-  static constexpr int kPitch = D + 8;    // K tile [kBN][kPitch]
-  static constexpr int vPitch = kBN + 8;  // V^T tile [D][vPitch]
+  static constexpr int kPitch = D + 8;
+  static constexpr int vPitch = ((D / 2) % 64 == 16 || (D / 2) % 64 == 48) ? D : D + 32;
   static constexpr int kElems = kBN * kPitch;
-  static constexpr int vElems = D * vPitch;
+  static constexpr int vElems = kBN * vPitch;
 };
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j % 4
+// of the 8-byte chunks addressed by lanes 4i + j / 4, i = 0..3 (element i of
+// the result). Lanes 4i + s that address row (key) r0 + i, dims d0 + 4s .. +3
+// therefore give lane j dims d0 + j of keys r0 .. r0 + 3.
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (v4s __attribute__((address_space(3)))*)(const_cast<uint16_t*>(p)));
+  return __builtin_bit_cast(u32x2, r);
+}
 
 #ifndef VRH_PREFILL_WG_PER_CU
 #define VRH_PREFILL_WG_PER_CU 2
@@ -135,12 +144,10 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
   constexpr int KCH = D / 8;                // 16-byte chunks per K row
   constexpr int KVECS = kBN * KCH;               // K tile 16-byte vectors
   constexpr int KLOADS = (KVECS + kThreads - 1) / kThreads;  // per thread
-  constexpr int VUNITS = (kBN / 4) * KCH;       // (4 keys x 8 dims) units per V tile
-  constexpr int VLOADS = (VUNITS + kThreads - 1) / kThreads;
   static_assert(D % 32 == 0 && D <= 224, "head_dim");
 
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][Lds<D>::kElems];
-  __shared__ __attribute__((aligned(16))) uint16_t vts[2][Lds<D>::vElems];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[2][Lds<D>::vElems];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -204,7 +211,7 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
   // One tile of staged K/V in registers.
   struct Regs {
     u32x4 k[KLOADS];
-    u32x4 v[VLOADS][4];
+    u32x4 v[KLOADS];
   };
   // A 512-entry segment of the page table is staged in LDS. A page id
   // fetched with a vector load would make every later K/V load wait for all
@@ -242,48 +249,27 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
     for (int r = 0; r < KLOADS; ++r) {
       const int c = min(tid + kThreads * r, KVECS - 1);
       const int pos = min(t0 + c / KCH, end - 1);
-      R.k[r] = load_cached(
-          reinterpret_cast<const u32x4*>(kg + slot(pos, a.k_block, a.k_token) + (c % KCH) * 8));
-    }
-#pragma unroll
-    for (int r = 0; r < VLOADS; ++r) {
-      const int u = min(tid + kThreads * r, VUNITS - 1);
-      const int kq = u / KCH, dc = u % KCH;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int pos = min(t0 + 4 * kq + j, end - 1);
-        R.v[r][j] = load_cached(
-            reinterpret_cast<const u32x4*>(vg + slot(pos, a.v_block, a.v_token) + dc * 8));
-      }
+      const int pg = page_of(pos);
+      const int off = pos - pg * a.block_size;
+      const int64_t page = tbl_lds[pg - tbl_base];
+      const int dof = (c % KCH) * 8;
+      R.k[r] = load_cached(reinterpret_cast<const u32x4*>(kg + page * a.k_block +
+                                                          (int64_t)off * a.k_token + dof));
+      R.v[r] = load_cached(reinterpret_cast<const u32x4*>(vg + page * a.v_block +
+                                                          (int64_t)off * a.v_token + dof));
     }
   };
-  // Registers -> LDS stage: K row-major, V transposed to [d][key] with the
-  // column swizzle of vt_group (2 passes per wave write, the minimum).
+  // Registers -> LDS stage, K and V alike: 16 lanes write one key row.
   auto stash = [&](int stage, const Regs& R) {
     uint16_t* kd = ks[stage];
-    uint16_t* vd = vts[stage];
+    uint16_t* vd = vs[stage];
 #pragma unroll
     for (int r = 0; r < KLOADS; ++r) {
       const int c = tid + kThreads * r;
-      if (KVECS % kThreads == 0 || c < KVECS)
-        *reinterpret_cast<u32x4*>(&kd[(c / KCH) * Lds<D>::kPitch + (c % KCH) * 8]) = R.k[r];
-    }
-#pragma unroll
-    for (int r = 0; r < VLOADS; ++r) {
-      const int u = tid + kThreads * r;
-      if (u < VUNITS) {
-        const int kq = u / KCH, dc = u % KCH;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {  // dim dc*8 + e, keys 4kq .. 4kq+3
-          const int w = e >> 1;
-          // v_perm_b32: low or high 16-bit halves of two words -> one word.
-          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-          const uint32_t k01 = __builtin_amdgcn_perm(R.v[r][1][w], R.v[r][0][w], sel);
-          const uint32_t k23 = __builtin_amdgcn_perm(R.v[r][3][w], R.v[r][2][w], sel);
-          const int d = dc * 8 + e;
-          *reinterpret_cast<u32x2*>(&vd[d * Lds<D>::vPitch + 4 * vt_group(d, kq)]) =
-              u32x2{k01, k23};
-        }
+      if (KVECS % kThreads == 0 || c < KVECS) {
+        const int row = c / KCH, dof = (c % KCH) * 8;
+        *reinterpret_cast<u32x4*>(&kd[row * Lds<D>::kPitch + dof]) = R.k[r];
+        *reinterpret_cast<u32x4*>(&vd[row * Lds<D>::vPitch + dof]) = R.v[r];
       }
     }
   };
@@ -293,7 +279,7 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
   auto compute = [&](int t) {
     const int stage = t & 1;
     const uint16_t* kd = ks[stage];
-    const uint16_t* vd = vts[stage];
+    const uint16_t* vd = vs[stage];
 #pragma unroll
     for (int kb = 0; kb < kBN / 32; ++kb) {
       const int k0 = t * kBN + 32 * kb;  // first key of the sub-block
@@ -352,17 +338,20 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
         pop[c] = u32x4{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
                        pack2<T>(p[6], p[7])};
       }
-      // O^T[d, q] += V^T[d, keys] P^T[keys, q], A-operand keys matching pop's.
+      // O^T[d, q] += V^T[d, keys] P^T[keys, q]. A-operand lane l needs dim
+      // 32db + l % 32 at pop's keys 16c + 4half + {0..3} and 16c + 8 + 4half +
+      // {0..3}: two transposed reads whose 16-lane group g covers dims
+      // 32db + 16(g & 1) .. +15 (lanes 4i + s address key i, dims +4s).
+      const int tr_row = 32 * kb + 4 * half + ((lane & 15) >> 2);
+      const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const int d = 32 * db + col;
-        const uint16_t* vrow = &vd[d * Lds<D>::vPitch];
         u32x4 vop[2];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {  // key groups 8kb + 4c + half and + 2
-          const int g = 8 * kb + 4 * c + half;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + 4 * vt_group(d, g));
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 4 * vt_group(d, g + 2));
+        for (int c = 0; c < 2; ++c) {
+          const uint16_t* vp = &vd[(tr_row + 16 * c) * Lds<D>::vPitch + 32 * db + tr_col];
+          const u32x2 lo = lds_read_tr16(vp);
+          const u32x2 hi = lds_read_tr16(vp + 8 * Lds<D>::vPitch);
           vop[c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
 #pragma unroll
