@@ -25,6 +25,7 @@
 // kernel over the expanded rows: query i of sequence s is a decode row with
 // length n_s - q_s + i + 1 (the per-row formulation the reference tests use).
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -81,10 +82,6 @@ struct Mfma<f16_t> {
   }
 };
 
-// K/V tiles are re-read by every query block of a sequence: normal (cached)
-// loads, so the XCD's L2 serves the repeats.
-__device__ __forceinline__ u32x4 load_cached(const u32x4* p) { return *p; }
-
 struct PrefillArgs {
   void* out;
   const void* q;
@@ -101,23 +98,46 @@ struct PrefillArgs {
   int32_t qblocks, kv_heads;
   int32_t group, block_size, bs_shift, table_width;
   int32_t skip_q;  // sequences with q_len <= skip_q are left to the decode kernel
+  int32_t uniform_pages;  // block size a power-of-two multiple of 256 / (16-byte chunks per row)
   float scale_log2;
 };
 
-// LDS tiles, two stages each, both row-major [key][d].
-//  * K rows are padded by 16 bytes so the 32 rows an MFMA operand read touches
-//    spread over the banks.
-//  * V is read with ds_read_b64_tr_b16, which hands each lane of a 16-lane
-//    group one dim of four consecutive keys (the transposed operand). One
-//    wave read covers 8 rows x 64 contiguous bytes; a row pitch of 16 or 48
-//    words mod 64 puts those 8 row segments on distinct banks.
+// LDS tiles, two stages each, K and V both row-major [key][d] without
+// padding: the tiles are filled by LDS-DMA loads, whose destination is 64
+// consecutive 16-byte slots per instruction. Bank conflicts are removed by an
+// XOR swizzle of the 16-byte chunk index inside each row instead:
+// chunk c of row r is stored at slot c ^ swizzle(r). For 256-byte rows
+// (D = 128) swizzle(r) = ((r & 3) << 2) ^ ((r >> 2) & 3) serves both readers
+// at the full 256 B/clk: the K operand read (32 rows, one chunk each) and the
+// transposed V read (8 rows x 4 chunks). Narrower rows pack 256 / (16 * KCH)
+// rows into one bank window and swizzle on the window index instead.
 template <int D>
 struct Lds {
-  static constexpr int kPitch = D + 8;
-  static constexpr int vPitch = ((D / 2) % 64 == 16 || (D / 2) % 64 == 48) ? D : D + 32;
-  static constexpr int kElems = kBN * kPitch;
-  static constexpr int vElems = kBN * vPitch;
+  static constexpr int KCH = D / 8;  // 16-byte chunks per row
+  static constexpr int kElems = kBN * D;
+  static constexpr int vElems = kBN * D;
+  __device__ static int swizzle(int row) {
+    if constexpr (KCH == 16) return ((row & 3) << 2) ^ ((row >> 2) & 3);
+    else if constexpr (KCH == 8) return (((row >> 1) & 1) << 2) ^ ((row >> 2) & 3);
+    else if constexpr (KCH == 4) return (row >> 2) & 3;
+    else if constexpr (KCH % 8 == 0) return row & 7;
+    else return row & 3;  // KCH = 12, 20, 28: XOR stays inside 4-chunk groups
+  }
+  // Element offset of dim `d` of key row `row` (d % 8 kept inside its chunk).
+  __device__ static int at(int row, int d) {
+    return row * D + (((d >> 3) ^ swizzle(row)) << 3) + (d & 7);
+  }
 };
+
+// LDS-DMA: each lane's 16 bytes at `src` go to LDS byte address
+// m0 + 16 * lane (the tile slot of this instruction). Issued as inline
+// assembly so the compiler does not track it: the kernel itself waits
+// (vmcnt) before the barrier that publishes a stage.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds_base) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j % 4
 // of the 8-byte chunks addressed by lanes 4i + j / 4, i = 0..3 (element i of
@@ -142,9 +162,10 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
   constexpr int DC = D / 16;                // 16-wide d chunks (QK^T k-steps)
   constexpr int DB = D / 32;                // 32-row d blocks of O^T
   constexpr int KCH = D / 8;                // 16-byte chunks per K row
-  constexpr int KVECS = kBN * KCH;               // K tile 16-byte vectors
-  constexpr int KLOADS = (KVECS + kThreads - 1) / kThreads;  // per thread
+  constexpr int KINST = kBN * KCH / kThreads;  // DMA instructions per wave per tile (K, V each)
   static_assert(D % 32 == 0 && D <= 224, "head_dim");
+  static_assert(kBN * KCH % kThreads == 0, "tile");
+  using L = Lds<D>;
 
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][Lds<D>::kElems];
   __shared__ __attribute__((aligned(16))) uint16_t vs[2][Lds<D>::vElems];
@@ -208,11 +229,6 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
   const T* kg = reinterpret_cast<const T*>(a.k) + kvh * a.k_head;
   const T* vg = reinterpret_cast<const T*>(a.v) + kvh * a.v_head;
 
-  // One tile of staged K/V in registers.
-  struct Regs {
-    u32x4 k[KLOADS];
-    u32x4 v[KLOADS];
-  };
   // A 512-entry segment of the page table is staged in LDS. A page id
   // fetched with a vector load would make every later K/V load wait for all
   // earlier ones (vmcnt retires in order), so the per-key lookups read LDS;
@@ -232,54 +248,83 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
     else return pos >> a.bs_shift;
   };
   load_table(0);
-  // Global -> registers for tile `t`. Branch-free: keys past `end` re-read key
-  // end - 1 (real data); the softmax masks them, so P is 0 there.
-  auto fetch = [&](int t, Regs& R) {
+  // Global -> LDS stage for tile `t` by DMA. Instruction r of this wave fills
+  // slots 64 * (wave + 4r) .. + 63 of the tile: slot v holds chunk
+  // (v % KCH) ^ swizzle(row) of key row v / KCH. Branch-free: keys past `end`
+  // re-read key end - 1 (real data); the softmax masks them, so P is 0 there.
+  // With KCH a power of two a lane keeps its chunk and its row advances by
+  // S = 256 / KCH per instruction, so the swizzled chunk offset and the row
+  // term of the address are per-lane constants. When the block size is a
+  // multiple of S, the S rows of one instruction share a page: a full tile
+  // then needs one (wave-uniform) page-id read per instruction.
+  constexpr bool kPow2 = (KCH & (KCH - 1)) == 0;
+  constexpr int S = 256 / KCH;
+  const int lane_row = (64 * wave + lane) / KCH;
+  const int lane_dof = kPow2 ? (((64 * wave + lane) % KCH) ^ L::swizzle(lane_row)) * 8 : 0;
+  const T* lane_k = kg + (int64_t)lane_row * a.k_token + lane_dof;
+  const T* lane_v = vg + (int64_t)lane_row * a.v_token + lane_dof;
+  auto fetch = [&](int t, auto stage_c) {
+    constexpr int stage = decltype(stage_c)::value;
     const int t0 = t * kBN;
     {
       const int last_page = page_of(min(t0 + kBN, end) - 1);
       if (last_page >= tbl_base + kTableSeg) load_table(page_of(t0));
     }
-    auto slot = [&](int pos, int64_t block_stride, int64_t token_stride) {
-      const int pg = page_of(pos);
-      const int off = pos - pg * a.block_size;
-      return (int64_t)tbl_lds[pg - tbl_base] * block_stride + (int64_t)off * token_stride;
-    };
+    const uint32_t kbase = (uint32_t)(uintptr_t)ks[stage];
+    const uint32_t vbase = (uint32_t)(uintptr_t)vs[stage];
+    if (kPow2 && a.uniform_pages && t0 + kBN <= end) {
 #pragma unroll
-    for (int r = 0; r < KLOADS; ++r) {
-      const int c = min(tid + kThreads * r, KVECS - 1);
-      const int pos = min(t0 + c / KCH, end - 1);
-      const int pg = page_of(pos);
-      const int off = pos - pg * a.block_size;
-      const int64_t page = tbl_lds[pg - tbl_base];
-      const int dof = (c % KCH) * 8;
-      R.k[r] = load_cached(reinterpret_cast<const u32x4*>(kg + page * a.k_block +
-                                                          (int64_t)off * a.k_token + dof));
-      R.v[r] = load_cached(reinterpret_cast<const u32x4*>(vg + page * a.v_block +
-                                                          (int64_t)off * a.v_token + dof));
-    }
-  };
-  // Registers -> LDS stage, K and V alike: 16 lanes write one key row.
-  auto stash = [&](int stage, const Regs& R) {
-    uint16_t* kd = ks[stage];
-    uint16_t* vd = vs[stage];
-#pragma unroll
-    for (int r = 0; r < KLOADS; ++r) {
-      const int c = tid + kThreads * r;
-      if (KVECS % kThreads == 0 || c < KVECS) {
-        const int row = c / KCH, dof = (c % KCH) * 8;
-        *reinterpret_cast<u32x4*>(&kd[row * Lds<D>::kPitch + dof]) = R.k[r];
-        *reinterpret_cast<u32x4*>(&vd[row * Lds<D>::vPitch + dof]) = R.v[r];
+      for (int r = 0; r < KINST; ++r) {
+        const int inst = wave + 4 * r;
+        const int pb = t0 + r * S;  // first row of this instruction's rows
+        const int pg = pb >> a.bs_shift;
+        const int64_t page = __builtin_amdgcn_readfirstlane(tbl_lds[pg - tbl_base]);
+        const int64_t row_off = pb & (a.block_size - 1);
+        const uint32_t slot = (uint32_t)__builtin_amdgcn_readfirstlane(1024 * inst);
+        dma16(lane_k + (page * a.k_block + row_off * a.k_token), kbase + slot);
+        dma16(lane_v + (page * a.v_block + row_off * a.v_token), vbase + slot);
       }
+      return;
+    }
+#pragma unroll
+    for (int r = 0; r < KINST; ++r) {
+      const int inst = wave + 4 * r;
+      const int v = 64 * inst + lane;
+      const int row = kPow2 ? lane_row + r * S : v / KCH;
+      const int dof = kPow2 ? 0 : ((v % KCH) ^ L::swizzle(row)) * 8;
+      const int pos = min(t0 + row, end - 1);
+      const int pg = page_of(pos);
+      const int64_t page = tbl_lds[pg - tbl_base];
+      // lane_k / lane_v already hold lane_row tokens (pow2) or nothing else.
+      const int64_t toks = pos - pg * a.block_size - (kPow2 ? lane_row : 0);
+      const uint32_t slot = (uint32_t)__builtin_amdgcn_readfirstlane(1024 * inst);
+      const T* kp = (kPow2 ? lane_k : kg) + page * a.k_block + toks * a.k_token + dof;
+      const T* vp = (kPow2 ? lane_v : vg) + page * a.v_block + toks * a.v_token + dof;
+      dma16(kp, kbase + slot);
+      dma16(vp, vbase + slot);
     }
   };
 
+  // Per-lane LDS byte offsets inside a tile (the swizzle depends on row & 15,
+  // which the sub-block and 16-key steps below leave unchanged):
+  //  * K operand reads: row `col`, dims 16c + 8half;
+  //  * transposed V reads: rows 4half + (lane & 15) / 4 (+ 8), dims 32db + tr_col.
+  const int tr_row = 4 * half + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  uint32_t koff[DC], voff[DB][2];
+#pragma unroll
+  for (int c = 0; c < DC; ++c) koff[c] = 2 * L::at(col, 16 * c + 8 * half);
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) voff[db][h] = 2 * L::at(tr_row + 8 * h, 32 * db + tr_col);
+
   // One 64-key LDS tile is consumed as 32-key sub-blocks, each a full online
   // softmax step: only one S^T accumulator and two P^T operands are live.
-  auto compute = [&](int t) {
-    const int stage = t & 1;
-    const uint16_t* kd = ks[stage];
-    const uint16_t* vd = vs[stage];
+  auto compute = [&](int t, auto stage_c) {
+    constexpr int stage = decltype(stage_c)::value;
+    const char* kd = reinterpret_cast<const char*>(ks[stage]);
+    const char* vd = reinterpret_cast<const char*>(vs[stage]);
 #pragma unroll
     for (int kb = 0; kb < kBN / 32; ++kb) {
       const int k0 = t * kBN + 32 * kb;  // first key of the sub-block
@@ -290,8 +335,7 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
         u32x4 kop[4];  // A-operand reads in groups of 4, then their MFMAs
 #pragma unroll
         for (int c = 0; c < 4 && c0 + c < DC; ++c)
-          kop[c] = *reinterpret_cast<const u32x4*>(
-              &kd[(32 * kb + col) * Lds<D>::kPitch + 16 * (c0 + c) + 8 * half]);
+          kop[c] = *reinterpret_cast<const u32x4*>(kd + koff[c0 + c] + 32 * kb * D * 2);
 #pragma unroll
         for (int c = 0; c < 4 && c0 + c < DC; ++c) st = Mfma<T>::run(kop[c], qop[c0 + c], st);
       }
@@ -342,16 +386,14 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
       // 32db + l % 32 at pop's keys 16c + 4half + {0..3} and 16c + 8 + 4half +
       // {0..3}: two transposed reads whose 16-lane group g covers dims
       // 32db + 16(g & 1) .. +15 (lanes 4i + s address key i, dims +4s).
-      const int tr_row = 32 * kb + 4 * half + ((lane & 15) >> 2);
-      const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         u32x4 vop[2];
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          const uint16_t* vp = &vd[(tr_row + 16 * c) * Lds<D>::vPitch + 32 * db + tr_col];
-          const u32x2 lo = lds_read_tr16(vp);
-          const u32x2 hi = lds_read_tr16(vp + 8 * Lds<D>::vPitch);
+          const char* vp = vd + (32 * kb + 16 * c) * D * 2;
+          const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][0]));
+          const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][1]));
           vop[c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
 #pragma unroll
@@ -361,23 +403,26 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
   };
 
 
-  // Pipeline: tile t is consumed from LDS stage t % 2 while tile t + 1 sits
-  // in the other stage and tile t + 2 is in flight into registers. One
-  // barrier per tile separates "everyone finished tile t - 1" from
-  // overwriting its stage.
-  Regs ra;
-  if (tiles > 0) {
-    fetch(0, ra);
-    stash(0, ra);
-    if (tiles > 1) fetch(1, ra);
-  }
-  for (int t = 0; t < tiles; ++t) {
+  // Pipeline: tile t is consumed from LDS stage t % 2 while the DMA of tile
+  // t + 1 fills the other stage. Per tile: wait for this wave's DMA of tile t,
+  // barrier (every wave's part of tile t has landed and every wave is done
+  // with tile t - 1, whose stage the next DMA overwrites), issue tile t + 1,
+  // compute tile t.
+  // The loop is unrolled by two so that each stage's LDS addresses are
+  // compile-time offsets.
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  if (tiles > 0) fetch(0, S0{});
+  for (int t = 0; t < tiles; t += 2) {
+    dma_wait();
     __syncthreads();
-    if (t + 1 < tiles) {
-      stash((t & 1) ^ 1, ra);
-      if (t + 2 < tiles) fetch(t + 2, ra);
-    }
-    compute(t);
+    if (t + 1 < tiles) fetch(t + 1, S1{});
+    compute(t, S0{});
+    if (t + 1 >= tiles) break;
+    dma_wait();
+    __syncthreads();
+    if (t + 2 < tiles) fetch(t + 2, S0{});
+    compute(t + 1, S1{});
   }
   lsum += shfl_xor_f32(lsum, 32);
   if (!q_ok) return;
@@ -502,6 +547,12 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.table_width = table_width;
   a.skip_q = route_decode ? kDecodeQ : 0;
+  {
+    // Rows per DMA instruction step in the kernel: 256 / (head_dim / 8).
+    const int chunks = head_dim / 8;
+    const bool pow2_chunks = (chunks & (chunks - 1)) == 0;
+    a.uniform_pages = pow2_chunks && a.bs_shift >= 0 && block_size % (256 / chunks) == 0;
+  }
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
   a.num_seqs = num_seqs;
   a.kv_heads = kv_heads;
