@@ -112,7 +112,10 @@ int vrh_paged_decode(int dtype, void* out, const void* q, const void* key_cache,
  * the decode kernel. With a workspace of
  * vrh_paged_prefill_workspace_bytes(num_seqs, q_heads, head_dim) bytes,
  * sequences of one query (decode rows riding in a packed batch) use split-KV
- * decode; with none (NULL, 0) every sequence goes through the MFMA tiles. */
+ * decode, and the MFMA work items are dispatched longest sequence first (a
+ * small ranking kernel writes the order into the workspace; batches of up to
+ * 2048 sequences). With none (NULL, 0) every sequence goes through the MFMA
+ * tiles in batch order. Results do not depend on the order. */
 size_t vrh_paged_prefill_workspace_bytes(int64_t num_seqs, int32_t q_heads, int32_t head_dim);
 int vrh_paged_prefill(int dtype, void* out, const void* q, const void* key_cache,
                       const void* value_cache, const int32_t* block_tables,

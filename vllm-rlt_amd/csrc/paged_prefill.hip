@@ -99,6 +99,7 @@ struct PrefillArgs {
   int32_t group, block_size, bs_shift, table_width;
   int32_t skip_q;  // sequences with q_len <= skip_q are left to the decode kernel
   int32_t uniform_pages;  // block size a power-of-two multiple of 256 / (16-byte chunks per row)
+  const int32_t* order;   // sequences in dispatch order (longest first), or null
   float scale_log2;
 };
 
@@ -185,7 +186,7 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
   const int64_t g = (slot / per_group) * 8 + blockIdx.x % 8;
   if (g >= a.num_seqs * a.kv_heads) return;
   const int r_item = (int)(slot % per_group);
-  const int64_t seq = g / a.kv_heads;
+  const int64_t seq = a.order ? a.order[g / a.kv_heads] : g / a.kv_heads;
   const int head = (int)(g % a.kv_heads) * a.group + r_item / a.qblocks;
   const int qb = a.qblocks - 1 - r_item % a.qblocks;
   const int kvh = head / a.group;
@@ -440,6 +441,34 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
   }
 }
 
+// Longest-first dispatch order of the sequences (list scheduling: a work item
+// of n keys costs ~n / 64 tiles, and the hardware starts workgroups in id
+// order as slots free up, so the long items must not come last). Rank sort
+// in one workgroup: rank(i) = #{j : key_j > key_i or (key_j == key_i and
+// j < i)}, so equal keys keep their order and the permutation is stable.
+// key = clamped length, or -1 for sequences the MFMA kernel skips.
+constexpr int kOrderMax = 2048;  // larger batches keep the identity order
+__global__ __launch_bounds__(1024) void prefill_order_kernel(const int32_t* cu, const int32_t* lengths,
+                                                             int32_t num_seqs, int32_t skip_q,
+                                                             int64_t cap, int32_t* order) {
+  __shared__ int32_t key[kOrderMax];
+  for (int i = threadIdx.x; i < num_seqs; i += blockDim.x) {
+    const int q_len = cu[i + 1] - cu[i];
+    const int64_t n = lengths[i];
+    key[i] = q_len <= skip_q ? -1 : (int32_t)(n < 0 ? 0 : (n > cap ? cap : n));
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < num_seqs; i += blockDim.x) {
+    const int32_t ki = key[i];
+    int rank = 0;
+    for (int j = 0; j < num_seqs; ++j) {
+      const int32_t kj = key[j];
+      rank += (kj > ki) | ((kj == ki) & (j < i));
+    }
+    order[rank] = i;
+  }
+}
+
 template <typename T, int MODE>
 bool launch_prefill_d(int d, dim3 grid, hipStream_t s, const PrefillArgs& a) {
   switch (d) {
@@ -476,9 +505,15 @@ using namespace vrh;
 // batch) run through the split-KV decode kernel instead of 64-query MFMA tiles.
 constexpr int kDecodeQ = 1;
 
+// Workspace: split-KV partials of the decode rows, then the dispatch order
+// (int32 per sequence, 256-byte aligned).
+static size_t decode_part_bytes(int64_t num_seqs, int32_t q_heads, int32_t head_dim) {
+  return (vrh_paged_decode_workspace_bytes(num_seqs * kDecodeQ, q_heads, head_dim) + 255) / 256 * 256;
+}
+
 extern "C" size_t vrh_paged_prefill_workspace_bytes(int64_t num_seqs, int32_t q_heads,
                                                     int32_t head_dim) {
-  return vrh_paged_decode_workspace_bytes(num_seqs * kDecodeQ, q_heads, head_dim);
+  return decode_part_bytes(num_seqs, q_heads, head_dim) + (size_t)num_seqs * sizeof(int32_t);
 }
 
 extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void* key_cache,
@@ -557,6 +592,15 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   a.num_seqs = num_seqs;
   a.kv_heads = kv_heads;
   a.qblocks = ceil_div(max_seqlen_q, kBM);
+  a.order = nullptr;
+  if (route_decode && num_seqs > 1 && num_seqs <= kOrderMax) {
+    int32_t* order = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
+                                                decode_part_bytes(num_seqs, q_heads, head_dim));
+    hipLaunchKernelGGL(prefill_order_kernel, dim3(1), dim3(1024), 0, s, cu_seqlens_q,
+                       context_lengths, (int32_t)num_seqs, a.skip_q,
+                       (int64_t)table_width * block_size, order);
+    a.order = order;
+  }
   const int64_t groups = num_seqs * kv_heads;
   const int64_t launched = (groups + 7) / 8 * 8 * (int64_t)a.group * a.qblocks;
   VRH_CHECK_ARG(launched < (1ll << 31), "vrh_paged_prefill: too many work items");
@@ -571,7 +615,8 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
         (int32_t)num_seqs, kDecodeQ, num_seqs * kDecodeQ, q_heads, kv_heads, head_dim,
         block_size, table_width, table_stride, q_token_stride, q_head_stride, out_token_stride,
         out_head_stride, k_block_stride, k_token_stride, k_head_stride, v_block_stride,
-        v_token_stride, v_head_stride, 0, workspace, workspace_bytes, s, "vrh_paged_prefill");
+        v_token_stride, v_head_stride, 0, workspace,
+        decode_part_bytes(num_seqs, q_heads, head_dim), s, "vrh_paged_prefill");
     if (rc != VRH_OK) return rc;
   }
   VRH_RETURN_LAUNCH("vrh_paged_prefill");
