@@ -6,11 +6,13 @@
 // keys at positions <= that. fp32 online softmax; P is rounded to the storage
 // dtype before the PV product (as the reference's `weights.to(values.dtype)`).
 //
-// MFMA path (bf16/f16, head_dim a multiple of 32 up to 224, LDS-bound):
+// MFMA path (bf16/f16, head_dim a multiple of 32 up to 128):
 //  * Workgroup = 4 waves = 128 query rows of one (sequence, q head); each wave
-//    owns 32 queries. K/V tiles of 64 keys are staged in LDS (two stages) and
-//    shared by the 4 waves: tile t is consumed while tile t+1 sits in the other
-//    stage and tile t+2 is in flight into registers; one barrier per tile.
+//    owns 32 queries. K/V arrive in 32-key sub-blocks staged through
+//    registers into LDS (three stages) and shared by the 4 waves; one
+//    barrier per sub-block.
+//  * Each wave software-pipelines the sub-blocks: the QK^T MFMAs of sub-block
+//    j + 1 are interleaved with the softmax VALU work of sub-block j.
 //  * S^T = K Q^T with v_mfma_f32_32x32x16_{bf16,f16}: A = K rows from LDS
 //    (16-byte reads), B = Q^T held in registers for the whole kernel.
 //    Output lane l holds query l % 32 and keys 8 * (j / 4) + 4 * (l / 32) + j % 4.
@@ -20,7 +22,7 @@
 //    ds_read_b64_tr_b16 transposed reads whose keys match the P^T k-slots.
 //    Only the pairing of A and B k-slots matters, not the hardware's k order.
 //  * Per-query running max is reduced over the lane pair (l, l ^ 32) each
-//    tile; the running sum stays a per-lane partial until the end.
+//    sub-block; the running sum stays a per-lane partial until the end.
 // Other dtypes / head dims (f32 reference checks, odd dims) run the decode
 // kernel over the expanded rows: query i of sequence s is a decode row with
 // length n_s - q_s + i + 1 (the per-row formulation the reference tests use).
@@ -43,17 +45,16 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
 namespace vrh {
 namespace {
 
-#ifndef VRH_PREFILL_WAVES
-#define VRH_PREFILL_WAVES 4
-#endif
-#ifndef VRH_PREFILL_BN
-#define VRH_PREFILL_BN 64
-#endif
-constexpr int kWaves = VRH_PREFILL_WAVES;  // waves per workgroup
+constexpr int kWaves = 4;                  // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kWQ = 32;                    // queries per wave
 constexpr int kBM = kWQ * kWaves;          // queries per workgroup
-constexpr int kBN = VRH_PREFILL_BN;        // keys per tile
+constexpr int kSB = 32;                    // keys per sub-block (one pipeline step)
+#ifndef VRH_PREFILL_STAGES
+#define VRH_PREFILL_STAGES 3
+#endif
+constexpr int kStages = VRH_PREFILL_STAGES;  // LDS half-stages: one sub-block each
+static_assert(kStages >= 3 && kStages <= 4, "stages");
 constexpr int kTableSeg = 512;             // page ids staged in LDS at a time
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
@@ -103,10 +104,10 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-// LDS tiles, two stages each, K and V both row-major [key][d] without
-// padding: the tiles are filled by LDS-DMA loads, whose destination is 64
-// consecutive 16-byte slots per instruction. Bank conflicts are removed by an
-// XOR swizzle of the 16-byte chunk index inside each row instead:
+// LDS tiles (one 32-key sub-block of K and of V per stage), both row-major
+// [key][d] without padding: each 16-byte staging store of a wave fills 64
+// consecutive 16-byte slots. Bank conflicts are removed by an XOR swizzle of
+// the 16-byte chunk index inside each row instead:
 // chunk c of row r is stored at slot c ^ swizzle(r). For 256-byte rows
 // (D = 128) swizzle(r) = ((r & 3) << 2) ^ ((r >> 2) & 3) serves both readers
 // at the full 256 B/clk: the K operand read (32 rows, one chunk each) and the
@@ -115,8 +116,7 @@ struct PrefillArgs {
 template <int D>
 struct Lds {
   static constexpr int KCH = D / 8;  // 16-byte chunks per row
-  static constexpr int kElems = kBN * D;
-  static constexpr int vElems = kBN * D;
+  static constexpr int kElems = kSB * D;  // one sub-block of K (or V)
   __device__ static int swizzle(int row) {
     if constexpr (KCH == 16) return ((row & 3) << 2) ^ ((row >> 2) & 3);
     else if constexpr (KCH == 8) return (((row >> 1) & 1) << 2) ^ ((row >> 2) & 3);
@@ -129,16 +129,6 @@ struct Lds {
     return row * D + (((d >> 3) ^ swizzle(row)) << 3) + (d & 7);
   }
 };
-
-// LDS-DMA: each lane's 16 bytes at `src` go to LDS byte address
-// m0 + 16 * lane (the tile slot of this instruction). Issued as inline
-// assembly so the compiler does not track it: the kernel itself waits
-// (vmcnt) before the barrier that publishes a stage.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(src), "s"(lds_base) : "memory", "m0");
-}
-__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j % 4
 // of the 8-byte chunks addressed by lanes 4i + j / 4, i = 0..3 (element i of
@@ -159,17 +149,18 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
 enum PageMode { kDiv = 0, kShift = 1 };
 
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill_kernel(PrefillArgs a) {
-  constexpr int DC = D / 16;                // 16-wide d chunks (QK^T k-steps)
-  constexpr int DB = D / 32;                // 32-row d blocks of O^T
-  constexpr int KCH = D / 8;                // 16-byte chunks per K row
-  constexpr int KINST = kBN * KCH / kThreads;  // DMA instructions per wave per tile (K, V each)
-  static_assert(D % 32 == 0 && D <= 224, "head_dim");
-  static_assert(kBN * KCH % kThreads == 0, "tile");
+__global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU)
+__attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU))) void paged_prefill_kernel(PrefillArgs a) {
+  constexpr int DC = D / 16;                   // 16-wide d chunks (QK^T k-steps)
+  constexpr int DB = D / 32;                   // 32-row d blocks of O^T
+  constexpr int KCH = D / 8;                   // 16-byte chunks per key row
+  constexpr int SB_INST = kSB * KCH / 64;      // 16-byte wave stores per sub-block (K or V)
+  constexpr int NI = (SB_INST + kWaves - 1) / kWaves;  // per wave (the last may be idle)
+  static_assert(D % 32 == 0 && D <= 128, "head_dim");
   using L = Lds<D>;
 
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][Lds<D>::kElems];
-  __shared__ __attribute__((aligned(16))) uint16_t vs[2][Lds<D>::vElems];
+  __shared__ __attribute__((aligned(16))) uint16_t ks[kStages][L::kElems];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[kStages][L::kElems];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -199,12 +190,15 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
     n = n < 0 ? 0 : ((int64_t)n > cap ? (int)cap : n);
   }
   const int prefix = n - q_len;
-  const int qi = qb * kBM + wave * kWQ + col;  // this lane's query
+  const int qi0 = qb * kBM + wave * kWQ;        // this wave's first query
+  const int qi = qi0 + col;                     // this lane's query
   const bool q_ok = qi < q_len;
   const int qpos = prefix + qi;
-  const int wave_qpos0 = prefix + qb * kBM + wave * kWQ;
+  const int wave_qpos0 = prefix + qi0;
   const int end = max(0, min(n, prefix + (qb + 1) * kBM));
-  const int tiles = (end + kBN - 1) / kBN;
+  const int nsub = (end + kSB - 1) / kSB;       // sub-blocks staged by the workgroup
+  // Sub-blocks this wave computes: keys up to its last query's position.
+  const int nsub_w = qi0 >= q_len ? 0 : (max(0, min(end, wave_qpos0 + kWQ)) + kSB - 1) / kSB;
   const int32_t* table = a.tables + seq * a.table_stride;
 
   // Q^T B-operands: lane holds query `col`, dims 16c + 8*half .. +8.
@@ -233,8 +227,8 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
   // A 512-entry segment of the page table is staged in LDS. A page id
   // fetched with a vector load would make every later K/V load wait for all
   // earlier ones (vmcnt retires in order), so the per-key lookups read LDS;
-  // the segment is refilled (all waves, between barriers) when a tile's pages
-  // run past it.
+  // the segment is refilled (all waves, between barriers) when a sub-block's
+  // pages run past it.
   __shared__ int32_t tbl_lds[kTableSeg];
   int tbl_base = 0;
   auto load_table = [&](int base) {
@@ -249,65 +243,73 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
     else return pos >> a.bs_shift;
   };
   load_table(0);
-  // Global -> LDS stage for tile `t` by DMA. Instruction r of this wave fills
-  // slots 64 * (wave + 4r) .. + 63 of the tile: slot v holds chunk
-  // (v % KCH) ^ swizzle(row) of key row v / KCH. Branch-free: keys past `end`
-  // re-read key end - 1 (real data); the softmax masks them, so P is 0 there.
+
+  // Sub-block `j` of K/V: global -> registers (gather), registers -> LDS
+  // stage (put). Store r of this wave fills slots 64 * (wave + 4r) .. + 63 of
+  // the sub-block: slot v holds chunk (v % KCH) ^ swizzle(row) of key row
+  // v / KCH. Branch-free: keys past `end` re-read key end - 1 (real data);
+  // the softmax masks them.
   // With KCH a power of two a lane keeps its chunk and its row advances by
   // S = 256 / KCH per instruction, so the swizzled chunk offset and the row
   // term of the address are per-lane constants. When the block size is a
-  // multiple of S, the S rows of one instruction share a page: a full tile
-  // then needs one (wave-uniform) page-id read per instruction.
+  // multiple of S, the S rows of one instruction share a page: a full
+  // sub-block then needs one (wave-uniform) page-id read per instruction.
   constexpr bool kPow2 = (KCH & (KCH - 1)) == 0;
   constexpr int S = 256 / KCH;
   const int lane_row = (64 * wave + lane) / KCH;
   const int lane_dof = kPow2 ? (((64 * wave + lane) % KCH) ^ L::swizzle(lane_row)) * 8 : 0;
   const T* lane_k = kg + (int64_t)lane_row * a.k_token + lane_dof;
   const T* lane_v = vg + (int64_t)lane_row * a.v_token + lane_dof;
-  auto fetch = [&](int t, auto stage_c) {
-    constexpr int stage = decltype(stage_c)::value;
-    const int t0 = t * kBN;
+  struct Regs { u32x4 k[NI]; u32x4 v[NI]; };
+  auto gather = [&](int j, Regs& R) {
+    const int k0 = j * kSB;
     {
-      const int last_page = page_of(min(t0 + kBN, end) - 1);
-      if (last_page >= tbl_base + kTableSeg) load_table(page_of(t0));
+      const int last_page = page_of(min(k0 + kSB, end) - 1);
+      if (last_page >= tbl_base + kTableSeg) load_table(page_of(k0));
     }
-    const uint32_t kbase = (uint32_t)(uintptr_t)ks[stage];
-    const uint32_t vbase = (uint32_t)(uintptr_t)vs[stage];
-    if (kPow2 && a.uniform_pages && t0 + kBN <= end) {
+    auto pad = [&](int inst) { return SB_INST % kWaves != 0 && inst >= SB_INST; };
+    if (kPow2 && a.uniform_pages && k0 + kSB <= end) {
 #pragma unroll
-      for (int r = 0; r < KINST; ++r) {
-        const int inst = wave + 4 * r;
-        const int pb = t0 + r * S;  // first row of this instruction's rows
+      for (int r = 0; r < NI; ++r) {
+        const int inst = wave + kWaves * r;
+        if (pad(inst)) continue;
+        const int pb = k0 + r * S;
         const int pg = pb >> a.bs_shift;
         const int64_t page = __builtin_amdgcn_readfirstlane(tbl_lds[pg - tbl_base]);
         const int64_t row_off = pb & (a.block_size - 1);
-        const uint32_t slot = (uint32_t)__builtin_amdgcn_readfirstlane(1024 * inst);
-        dma16(lane_k + (page * a.k_block + row_off * a.k_token), kbase + slot);
-        dma16(lane_v + (page * a.v_block + row_off * a.v_token), vbase + slot);
+        R.k[r] = *reinterpret_cast<const u32x4*>(lane_k + (page * a.k_block + row_off * a.k_token));
+        R.v[r] = *reinterpret_cast<const u32x4*>(lane_v + (page * a.v_block + row_off * a.v_token));
       }
       return;
     }
 #pragma unroll
-    for (int r = 0; r < KINST; ++r) {
-      const int inst = wave + 4 * r;
+    for (int r = 0; r < NI; ++r) {
+      const int inst = wave + kWaves * r;
+      if (pad(inst)) continue;
       const int v = 64 * inst + lane;
       const int row = kPow2 ? lane_row + r * S : v / KCH;
       const int dof = kPow2 ? 0 : ((v % KCH) ^ L::swizzle(row)) * 8;
-      const int pos = min(t0 + row, end - 1);
+      const int pos = min(k0 + row, end - 1);
       const int pg = page_of(pos);
       const int64_t page = tbl_lds[pg - tbl_base];
-      // lane_k / lane_v already hold lane_row tokens (pow2) or nothing else.
       const int64_t toks = pos - pg * a.block_size - (kPow2 ? lane_row : 0);
-      const uint32_t slot = (uint32_t)__builtin_amdgcn_readfirstlane(1024 * inst);
-      const T* kp = (kPow2 ? lane_k : kg) + page * a.k_block + toks * a.k_token + dof;
-      const T* vp = (kPow2 ? lane_v : vg) + page * a.v_block + toks * a.v_token + dof;
-      dma16(kp, kbase + slot);
-      dma16(vp, vbase + slot);
+      R.k[r] = *reinterpret_cast<const u32x4*>((kPow2 ? lane_k : kg) + page * a.k_block + toks * a.k_token + dof);
+      R.v[r] = *reinterpret_cast<const u32x4*>((kPow2 ? lane_v : vg) + page * a.v_block + toks * a.v_token + dof);
+    }
+  };
+  auto put = [&](auto stage_c, const Regs& R) {
+    constexpr int stage = decltype(stage_c)::value;
+#pragma unroll
+    for (int r = 0; r < NI; ++r) {
+      const int inst = wave + kWaves * r;
+      if (SB_INST % kWaves != 0 && inst >= SB_INST) continue;
+      *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(ks[stage]) + 1024 * inst + 16 * lane) = R.k[r];
+      *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(vs[stage]) + 1024 * inst + 16 * lane) = R.v[r];
     }
   };
 
-  // Per-lane LDS byte offsets inside a tile (the swizzle depends on row & 15,
-  // which the sub-block and 16-key steps below leave unchanged):
+  // Per-lane LDS byte offsets inside a half-stage (the swizzle depends on
+  // row & 15, which the 16-key steps below leave unchanged):
   //  * K operand reads: row `col`, dims 16c + 8half;
   //  * transposed V reads: rows 4half + (lane & 15) / 4 (+ 8), dims 32db + tr_col.
   const int tr_row = 4 * half + ((lane & 15) >> 2);
@@ -320,110 +322,172 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
 #pragma unroll
     for (int h = 0; h < 2; ++h) voff[db][h] = 2 * L::at(tr_row + 8 * h, 32 * db + tr_col);
 
-  // One 64-key LDS tile is consumed as 32-key sub-blocks, each a full online
-  // softmax step: only one S^T accumulator and two P^T operands are live.
-  auto compute = [&](int t, auto stage_c) {
+  // S^T = K Q^T for the sub-block in half-stage `stage`: element j holds key
+  // 8(j/4) + 4half + j%4 of the sub-block for query `col`.
+  auto kload = [&](auto stage_c, u32x4 (&kop)[DC]) {
     constexpr int stage = decltype(stage_c)::value;
     const char* kd = reinterpret_cast<const char*>(ks[stage]);
+#pragma unroll
+    for (int c = 0; c < DC; ++c) kop[c] = *reinterpret_cast<const u32x4*>(kd + koff[c]);
+  };
+  auto qk_mfma = [&](const u32x4 (&kop)[DC]) {
+    f32x16 st = f32x16{};
+#pragma unroll
+    for (int c = 0; c < DC; ++c) st = Mfma<T>::run(kop[c], qop[c], st);
+    return st;
+  };
+  // V^T A-operands of the sub-block in half-stage `stage`: lane l needs dim
+  // 32db + l % 32 at keys 16c + 4half + {0..3} and 16c + 8 + 4half + {0..3}
+  // (pop's k-slots): two transposed reads whose 16-lane group g covers dims
+  // 32db + 16(g & 1) .. +15 (lanes 4i + s address key i, dims +4s).
+  auto vload = [&](auto stage_c, u32x4 (&vop)[DB][2]) {
+    constexpr int stage = decltype(stage_c)::value;
     const char* vd = reinterpret_cast<const char*>(vs[stage]);
 #pragma unroll
-    for (int kb = 0; kb < kBN / 32; ++kb) {
-      const int k0 = t * kBN + 32 * kb;  // first key of the sub-block
-      // S^T: element j holds key k0 + 8(j/4) + 4half + j%4 for query `col`.
-      f32x16 st = f32x16{};
-#pragma unroll
-      for (int c0 = 0; c0 < DC; c0 += 4) {
-        u32x4 kop[4];  // A-operand reads in groups of 4, then their MFMAs
-#pragma unroll
-        for (int c = 0; c < 4 && c0 + c < DC; ++c)
-          kop[c] = *reinterpret_cast<const u32x4*>(kd + koff[c0 + c] + 32 * kb * D * 2);
-#pragma unroll
-        for (int c = 0; c < 4 && c0 + c < DC; ++c) st = Mfma<T>::run(kop[c], qop[c0 + c], st);
-      }
-      // Causal mask only where needed (wave-uniform test: sub-blocks entirely
-      // below this wave's first query position and before `end` need none),
-      // then the raw running max over the lane pair (l, l ^ 32).
-      float mx = -INFINITY;
-      if (k0 + 32 <= end && k0 + 31 <= wave_qpos0) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[j]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int kpos = k0 + 8 * (j >> 2) + 4 * half + (j & 3);
-          const bool vis = q_ok && kpos < end && kpos <= qpos;
-          st[j] = vis ? st[j] : -INFINITY;
-          mx = fmaxf(mx, st[j]);
-        }
-      }
-      mx = fmaxf(mx, shfl_xor_f32(mx, 32));
-      // Lazy rescaling (log2 domain, m finite from the start): the reference
-      // max only moves when some lane's max grows by more than 8, so P stays
-      // <= 2^8 and most sub-blocks skip the O rescale.
-      const float mcand = mx * a.scale_log2;
-      if (__any(mcand > m + 8.f)) {
-        const float mnew = fmaxf(m, mcand);
-        const float corr = fast_exp2(m - mnew);
-        lsum *= corr;
-#pragma unroll
-        for (int t2 = 0; t2 < DB; ++t2) acc[t2] *= corr;
-        m = mnew;
-      }
-      // P^T B-operands per 16-key chunk c: elements 8c .. 8c+7 of st, i.e.
-      // keys k0 + 16c + 4half + {0..3} and k0 + 16c + 8 + 4half + {0..3}.
-      u32x4 pop[2];
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        float p[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          p[i] = fast_exp2(fmaf(st[8 * c + i], a.scale_log2, -m));
-          lsum += p[i];
-        }
-        pop[c] = u32x4{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
-                       pack2<T>(p[6], p[7])};
+        const char* vp = vd + 16 * c * D * 2;
+        const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][0]));
+        const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][1]));
+        vop[db][c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
-      // O^T[d, q] += V^T[d, keys] P^T[keys, q]. A-operand lane l needs dim
-      // 32db + l % 32 at pop's keys 16c + 4half + {0..3} and 16c + 8 + 4half +
-      // {0..3}: two transposed reads whose 16-lane group g covers dims
-      // 32db + 16(g & 1) .. +15 (lanes 4i + s address key i, dims +4s).
+  };
+  // P^T B-operands of scores `st` (already masked, m current): per 16-key
+  // chunk c, elements 8c .. 8c+7 of st, i.e. keys 16c + 4half + {0..3} and
+  // 16c + 8 + 4half + {0..3}.
+  auto probs = [&](const f32x16& st, u32x4 (&pop)[2]) {
+    float p[16];
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        u32x4 vop[2];
+    for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(st[i], a.scale_log2, -m));
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const char* vp = vd + (32 * kb + 16 * c) * D * 2;
-          const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][0]));
-          const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][1]));
-          vop[c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        }
+    for (int c = 0; c < 2; ++c)
+      pop[c] = u32x4{pack2<T>(p[8 * c], p[8 * c + 1]), pack2<T>(p[8 * c + 2], p[8 * c + 3]),
+                     pack2<T>(p[8 * c + 4], p[8 * c + 5]), pack2<T>(p[8 * c + 6], p[8 * c + 7])};
+    // Pairwise sum: a dependency chain of 4 adds instead of 16.
 #pragma unroll
-        for (int c = 0; c < 2; ++c) acc[db] = Mfma<T>::run(vop[c], pop[c], acc[db]);
+    for (int w = 1; w < 16; w *= 2)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2 * w) p[i] += p[i + w];
+    lsum += p[0];
+  };
+  auto pv = [&](const u32x4 (&vop)[DB][2], const u32x4 (&pop)[2]) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) acc[db] = Mfma<T>::run(vop[db][c], pop[c], acc[db]);
+  };
+  // Causal / end mask of sub-block j (only where needed: the wave-uniform
+  // test passes for sub-blocks entirely below this wave's first query and
+  // before `end`), the running max over the lane pair (l, l ^ 32), and the
+  // lazy rescale: the reference max (log2 domain, finite from the start)
+  // only moves when some lane's max grows by more than 8, so P stays <= 2^8
+  // and most sub-blocks skip the O rescale.
+  auto mask_max = [&](int j, f32x16& st) {
+    const int k0 = j * kSB;
+    float mx = -INFINITY;
+    if (k0 + kSB <= end && k0 + kSB - 1 <= wave_qpos0) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, st[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int kpos = k0 + 8 * (e >> 2) + 4 * half + (e & 3);
+        const bool vis = q_ok && kpos < end && kpos <= qpos;
+        st[e] = vis ? st[e] : -INFINITY;
+        mx = fmaxf(mx, st[e]);
       }
+    }
+    {
+      // Max with lane l ^ 32: one v_permlane32_swap gives both halves.
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                       false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    const float mcand = mx * a.scale_log2;
+    if (__any(mcand > m + 8.f)) {
+      const float mnew = fmaxf(m, mcand);
+      const float corr = fast_exp2(m - mnew);
+      lsum *= corr;
+#pragma unroll
+      for (int t2 = 0; t2 < DB; ++t2) acc[t2] *= corr;
+      m = mnew;
     }
   };
 
-
-  // Pipeline: tile t is consumed from LDS stage t % 2 while the DMA of tile
-  // t + 1 fills the other stage. Per tile: wait for this wave's DMA of tile t,
-  // barrier (every wave's part of tile t has landed and every wave is done
-  // with tile t - 1, whose stage the next DMA overwrites), issue tile t + 1,
-  // compute tile t.
-  // The loop is unrolled by two so that each stage's LDS addresses are
-  // compile-time offsets.
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  if (tiles > 0) fetch(0, S0{});
-  for (int t = 0; t < tiles; t += 2) {
-    dma_wait();
+  // Pipeline over 32-key sub-blocks, kStages (3 or 4) LDS stages, sub-block
+  // j in stage j % kStages. Step j:
+  //   barrier (sub-block j + 1, stored at step j - 1, is visible; every wave
+  //   has finished step j - 1, the last reader of sub-block j - 1);
+  //   store the registers holding sub-block j + 2 into stage (j + 2) %
+  //   kStages (which held sub-block j - 1 or j - 2), then gather sub-block
+  //   j + 3 into the same registers (one step of latency to land);
+  //   S1: every LDS operand read (K of j + 1, V of j), then the QK^T MFMAs of
+  //       j + 1 interleaved with the probability VALU work of j;
+  //   S2: PV of sub-block j (MFMA), then mask / max / rescale of j + 1.
+  // The loop is unrolled by kStages so every stage address is a
+  // compile-time offset.
+  using H0 = std::integral_constant<int, 0>;
+  using H1 = std::integral_constant<int, 1>;
+  using H2 = std::integral_constant<int, 2>;
+  using H3 = std::integral_constant<int, 3>;
+  f32x16 st = f32x16{};
+  Regs R;
+  if (nsub > 0) {
+    gather(0, R);
+    put(H0{}, R);
+    if (nsub > 1) { gather(1, R); put(H1{}, R); }
+    if (nsub > 2) gather(2, R);
     __syncthreads();
-    if (t + 1 < tiles) fetch(t + 1, S1{});
-    compute(t, S0{});
-    if (t + 1 >= tiles) break;
-    dma_wait();
-    __syncthreads();
-    if (t + 2 < tiles) fetch(t + 2, S0{});
-    compute(t + 1, S1{});
+    if (nsub_w > 0) {
+      u32x4 kop[DC];
+      kload(H0{}, kop);
+      st = qk_mfma(kop);
+      mask_max(0, st);
+    }
+    auto step = [&](int j, auto hc) {
+      constexpr int h = decltype(hc)::value;
+      using Hn = std::integral_constant<int, (h + 1) % kStages>;
+      using Hp = std::integral_constant<int, (h + 2) % kStages>;
+      __syncthreads();
+      if (j + 2 < nsub) put(Hp{}, R);
+      if (j + 3 < nsub) gather(j + 3, R);
+      if (j >= nsub_w) return;
+      u32x4 pop[2];
+      u32x4 vop[DB][2];
+      if (j + 1 < nsub_w) {
+        u32x4 kop[DC];
+        kload(Hn{}, kop);
+        vload(hc, vop);
+        __builtin_amdgcn_sched_barrier(0);
+        const f32x16 st_n = qk_mfma(kop);
+        probs(st, pop);
+#pragma unroll
+        for (int i = 0; i < DC; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        pv(vop, pop);
+        st = st_n;
+        mask_max(j + 1, st);
+      } else {
+        probs(st, pop);
+        vload(hc, vop);
+        pv(vop, pop);
+      }
+    };
+    for (int j = 0; j < nsub; j += kStages) {
+      step(j, H0{});
+      if (j + 1 >= nsub) break;
+      step(j + 1, H1{});
+      if (j + 2 >= nsub) break;
+      step(j + 2, H2{});
+      if constexpr (kStages > 3) {
+        if (j + 3 >= nsub) break;
+        step(j + 3, H3{});
+      }
+    }
   }
   lsum += shfl_xor_f32(lsum, 32);
   if (!q_ok) return;
@@ -432,11 +496,11 @@ __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU) void paged_prefill
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {  // rows 32db + 8g + 4half + {0..3}
-      const int d = 32 * db + 8 * g + 4 * half;
+    for (int gi = 0; gi < 4; ++gi) {  // rows 32db + 8gi + 4half + {0..3}
+      const int d = 32 * db + 8 * gi + 4 * half;
       *reinterpret_cast<u32x2*>(op + d) =
-          u32x2{pack2<T>(acc[db][4 * g] * inv, acc[db][4 * g + 1] * inv),
-                pack2<T>(acc[db][4 * g + 2] * inv, acc[db][4 * g + 3] * inv)};
+          u32x2{pack2<T>(acc[db][4 * gi] * inv, acc[db][4 * gi + 1] * inv),
+                pack2<T>(acc[db][4 * gi + 2] * inv, acc[db][4 * gi + 3] * inv)};
     }
   }
 }
@@ -480,11 +544,6 @@ bool launch_prefill_d(int d, dim3 grid, hipStream_t s, const PrefillArgs& a) {
     VRH_D(64)
     VRH_D(96)
     VRH_D(128)
-#if VRH_PREFILL_BN <= 64
-    VRH_D(160)
-    VRH_D(192)
-    VRH_D(224)
-#endif
 #undef VRH_D
     default: return false;
   }
@@ -539,7 +598,7 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
                 "vrh_paged_prefill: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const bool half = dtype == VRH_DTYPE_BF16 || dtype == VRH_DTYPE_F16;
-  bool mfma = half && head_dim % 32 == 0 && head_dim <= 224 && block_size >= 1 &&
+  bool mfma = half && head_dim % 32 == 0 && head_dim <= 128 && block_size >= 1 &&
               q_token_stride % 8 == 0 && q_head_stride % 8 == 0 && out_token_stride % 4 == 0 &&
               out_head_stride % 4 == 0 && k_block_stride % 8 == 0 && k_token_stride % 8 == 0 &&
               k_head_stride % 8 == 0 && v_block_stride % 8 == 0 && v_token_stride % 8 == 0 &&
