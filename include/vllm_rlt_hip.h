@@ -33,6 +33,14 @@
  *   vrh_expand_kv_addresses  kernels/metadata.py:7-24 (expand_kv_addresses)
  *   vrh_routing_metadata     kernels/routing.py:14-48 (metadata_kernel)
  *   vrh_routing_slots        kernels/routing.py:7-11 (slots_kernel)
+ *   vrh_kv_blocks_to_host    kv_cache_manager.py:481-502 (snapshot page copies)
+ *   vrh_kv_blocks_from_host  kv_cache_manager.py:504-523 (restore page copies)
+ *   vrh_gather_rows          kernels/routing.py:51-66 (gather_kernel)
+ *   vrh_scatter_rows         kernels/routing.py:69-83 (scatter_kernel)
+ *   vrh_gather_segments      kernels/routing.py:86-113 (gather_segments_kernel)
+ *   vrh_scatter_segments     kernels/routing.py:116-144 (scatter_segments_kernel)
+ *   vrh_silu_and_mul         csrc/activation/silu_and_mul.cu:221-245 (silu_and_mul_cuda),
+ *                            kernels/activation.py:20-33 (its Torch contract)
  */
 #ifndef VLLM_RLT_HIP_H_
 #define VLLM_RLT_HIP_H_
@@ -169,6 +177,57 @@ int vrh_kv_finalize_token(void* key_cache, void* value_cache, int64_t src_block,
 int vrh_kv_copy_blocks(void* key_cache, void* value_cache, int64_t block_stride_bytes,
                        int64_t block_bytes, const int64_t* src_blocks, const int64_t* dst_blocks,
                        int64_t n, vrh_stream_t stream);
+
+/* ------------------------------------------------------- host offload
+ * Preemption snapshot / restore of whole blocks (all layers) of both caches:
+ * to_host copies block blocks[i] of key_cache / value_cache to row i of
+ * host_keys / host_values (block_bytes per row); from_host copies row i back
+ * into block blocks[i]. blocks is a device array. The host rows must be pinned
+ * host memory (hipHostMalloc); the kernels access it through its device
+ * mapping, so no device staging buffer is allocated. Other pointers are
+ * rejected with VRH_ERROR_INVALID_ARG before any launch. Asynchronous on
+ * `stream`: the host rows are complete (to_host) or may be reused (from_host)
+ * once the stream has passed the call. Bit-exact. */
+int vrh_kv_blocks_to_host(const void* key_cache, const void* value_cache,
+                          int64_t block_stride_bytes, int64_t block_bytes, const int64_t* blocks,
+                          void* host_keys, void* host_values, int64_t n, vrh_stream_t stream);
+int vrh_kv_blocks_from_host(void* key_cache, void* value_cache, int64_t block_stride_bytes,
+                            int64_t block_bytes, const int64_t* blocks, const void* host_keys,
+                            const void* host_values, int64_t n, vrh_stream_t stream);
+
+/* ------------------------------------------------------ hidden-state rows
+ * Byte copies of `width_bytes`-wide rows (strides in bytes).
+ * gather_rows: out[r] = r < n ? pool[slots[r]] : 0 for r < size.
+ * scatter_rows: pool[slots[r]] = in[r] for r < count.
+ * segments: int64 [num_segments, 5] = (state_slot, hidden_row_offset,
+ * token_count, batch_row_start, keep_intermediate); pool row of segment row i
+ * is state_slot * pool_rows + hidden_row_offset + i, batch row is
+ * batch_row_start + i, i < token_count <= max_rows.
+ * gather_segments: out[batch row] = pool[pool row].
+ * scatter_segments: pool[pool row] = in[batch row] where keep_intermediate != 0. */
+int vrh_gather_rows(const void* pool, const int64_t* slots, void* out, int64_t n, int64_t size,
+                    int64_t width_bytes, int64_t pool_stride_bytes, int64_t out_stride_bytes,
+                    vrh_stream_t stream);
+int vrh_scatter_rows(const void* in, const int64_t* slots, void* pool, int64_t count,
+                     int64_t width_bytes, int64_t in_stride_bytes, int64_t pool_stride_bytes,
+                     vrh_stream_t stream);
+int vrh_gather_segments(const void* pool, const int64_t* segments, void* out,
+                        int64_t num_segments, int64_t max_rows, int64_t pool_rows,
+                        int64_t width_bytes, int64_t pool_stride_bytes, int64_t out_stride_bytes,
+                        vrh_stream_t stream);
+int vrh_scatter_segments(const void* in, const int64_t* segments, void* pool,
+                         int64_t num_segments, int64_t max_rows, int64_t pool_rows,
+                         int64_t width_bytes, int64_t in_stride_bytes, int64_t pool_stride_bytes,
+                         vrh_stream_t stream);
+
+/* ------------------------------------------------------------ SiLU-and-Mul
+ * out[i] = dtype(dtype(silu(gate[i])) * up[i]) for `count` contiguous elements
+ * (f32, f16, bf16). silu is evaluated so that its rounding to the dtype equals
+ * the double-precision value rounded to fp32 and then to the dtype; the
+ * product is rounded once. Pointers need only their dtype's alignment: gate,
+ * up and out may sit at different 16-byte offsets. */
+int vrh_silu_and_mul(int dtype, void* out, const void* gate, const void* up, int64_t count,
+                     vrh_stream_t stream);
 
 /* --------------------------------------------------------------- addresses
  * blocks[i] = tables[sequences[i] * width + positions[i] / page],

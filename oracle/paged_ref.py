@@ -213,3 +213,51 @@ def routing_slots(descriptors, n, size):
     for row in range(min(n, size)):
         out[row] = descriptors[row][0]
     return out
+
+
+# ------------------------------------------------- host offload (snapshot)
+def blocks_to_host(key_pool, value_pool, blocks):
+    """Rows of the snapshot: every page of the request in block-table order.
+
+    Follows core/kv_cache_manager.py:481-502 (``keys[row] = key_cache[block]``)."""
+    idx = np.asarray(blocks, dtype=np.int64)
+    return key_pool[idx].copy(), value_pool[idx].copy()
+
+
+def blocks_from_host(key_pool, value_pool, blocks, host_keys, host_values):
+    """core/kv_cache_manager.py:504-523: ``key_cache[block] = snapshot.keys[row]``."""
+    for row, block in enumerate(np.asarray(blocks, dtype=np.int64)):
+        key_pool[block] = host_keys[row]
+        value_pool[block] = host_values[row]
+
+
+# ------------------------------------------------------- hidden-state rows
+def gather_rows(pool, slots, n, size):
+    """kernels/routing.py:51-66 (gather_kernel): row r < size is pool[slots[r]]
+    when r < n, else zeros."""
+    out = np.zeros((size, pool.shape[1]), dtype=pool.dtype)
+    for r in range(min(n, size)):
+        out[r] = pool[slots[r]]
+    return out
+
+
+def scatter_rows(values, slots, pool, count):
+    """kernels/routing.py:69-83 (scatter_kernel): pool[slots[r]] = values[r], r < count."""
+    for r in range(count):
+        pool[slots[r]] = values[r]
+
+
+def gather_segments(pool, segments, out, pool_rows):
+    """kernels/routing.py:86-113 and its loop form in worker/model_runner.py:544-552."""
+    for slot, offset, count, start, _keep in np.asarray(segments, dtype=np.int64):
+        for i in range(count):
+            out[start + i] = pool[slot * pool_rows + offset + i]
+
+
+def scatter_segments(values, segments, pool, pool_rows):
+    """kernels/routing.py:116-144 and worker/model_runner.py:584-597 (keep only)."""
+    for slot, offset, count, start, keep in np.asarray(segments, dtype=np.int64):
+        if not keep:
+            continue
+        for i in range(count):
+            pool[slot * pool_rows + offset + i] = values[start + i]

@@ -211,3 +211,65 @@ def test_oracle_handles_fp16_widening(seed):
     half = [x.astype(np.float16).astype(np.float32) for x in (q, kc, vc)]
     out = ref.paged_attention(*half, tables, lengths)
     assert out.dtype == np.float32 and np.isfinite(out).all()
+
+
+# ------------------------------------------------------------ SiLU-and-Mul
+def test_silu_oracle_known_values():
+    # tests/test_activation.py:49-53 of the reference
+    from oracle import activation_ref as act
+
+    out = act.silu_and_mul(np.array([0.0, 1.0, -1.0], np.float32),
+                           np.array([2.0, 3.0, 4.0], np.float32), "f32")
+    np.testing.assert_allclose(out, [0.0, 2.1931758, -1.0757657], rtol=1e-6)
+
+
+def test_silu_oracle_matches_torch_float64_and_odd_identity():
+    from oracle import activation_ref as act
+
+    x = np.concatenate([np.linspace(-120, 120, 4001), [0.0, -0.0, 1e-30, -1e-30, 745.0, -745.0]])
+    ref64 = torch.nn.functional.silu(torch.tensor(x, dtype=torch.float64)).numpy()
+    got = act.silu_f64(x)
+    np.testing.assert_allclose(got, ref64, rtol=1e-14, atol=1e-300)  # x = -745: subnormal vs 0
+    # silu(x) - silu(-x) = x * (sigmoid(x) + sigmoid(-x)) = x: a sign or branch slip breaks it
+    np.testing.assert_allclose(got - act.silu_f64(-x), x, rtol=1e-12, atol=1e-300)
+    special = act.silu_f64(np.array([np.inf, -np.inf, np.nan]))
+    assert special[0] == np.inf and np.isnan(special[1]) and np.isnan(special[2])
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_silu_oracle_rounding_matches_torch_conversion_on_every_pattern(dtype):
+    # torch rounds float64 -> storage dtype through float32; the oracle must too,
+    # and the product path rounds once more (tests/test_activation.py:60-64).
+    from oracle import activation_ref as act
+
+    tdtype = torch.bfloat16 if dtype == "bf16" else torch.float16
+    patterns = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(tdtype)
+    gate = patterns.float().numpy()
+    up = np.full_like(gate, 1.5, dtype=np.float32)
+    g64 = patterns.double()
+    expected_act = (g64 * torch.sigmoid(g64)).to(tdtype)
+    expected = (expected_act.double() * 1.5).to(tdtype).float().numpy()
+    got = act.silu_and_mul(gate, up, dtype)
+    finite = ~np.isnan(expected)
+    assert np.array_equal(np.isnan(got), ~finite)
+    assert np.array_equal(got[finite].view(np.uint32), expected[finite].view(np.uint32))
+
+
+# ------------------------------------------------------- hidden-state rows
+def test_row_and_segment_oracle_literal_vectors():
+    pool = np.arange(24, dtype=np.int64).reshape(8, 3)
+    out = ref.gather_rows(pool, np.array([5, 0, 7, 9]), 3, 4)
+    assert out.tolist() == [[15, 16, 17], [0, 1, 2], [21, 22, 23], [0, 0, 0]]
+    target = np.zeros((8, 3), np.int64)
+    ref.scatter_rows(np.array([[1, 2, 3], [4, 5, 6]]), np.array([6, 1]), target, 2)
+    assert target[6].tolist() == [1, 2, 3] and target[1].tolist() == [4, 5, 6]
+    assert target.sum() == 21
+    # two state slots of 4 rows each; segments (slot, offset, count, start, keep)
+    segments = np.array([[1, 1, 2, 0, 1], [0, 3, 1, 2, 0]])
+    batch = np.full((3, 3), -1, np.int64)
+    ref.gather_segments(pool, segments, batch, 4)
+    assert batch.tolist() == [[15, 16, 17], [18, 19, 20], [9, 10, 11]]
+    back = np.zeros_like(pool)
+    ref.scatter_segments(batch, segments, back, 4)
+    assert back[5].tolist() == [15, 16, 17] and back[6].tolist() == [18, 19, 20]
+    assert back[3].tolist() == [0, 0, 0]  # keep = 0: not stored

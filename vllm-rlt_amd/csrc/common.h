@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 #include "vllm_rlt_hip.h"
 
 namespace vrh {
@@ -83,6 +85,30 @@ template <>
 struct RawVec<16> {
   using type = __attribute__((ext_vector_type(4))) uint32_t;
 };
+
+template <int VB>
+using raw_of = typename RawVec<VB>::type;
+
+// Widest byte-copy vector (16, 8, 4, 2 or 1) dividing every size and pointer.
+inline int pick_vb(std::initializer_list<int64_t> values, std::initializer_list<const void*> ptrs) {
+  for (int vb = 16; vb > 1; vb >>= 1) {
+    bool ok = true;
+    for (int64_t s : values) ok = ok && (s % vb == 0);
+    for (const void* p : ptrs) ok = ok && ((uintptr_t)p % vb == 0);
+    if (ok) return vb;
+  }
+  return 1;
+}
+
+// Launch KERNEL<vb> for a runtime byte-vector width.
+#define VRH_DISPATCH_VB(vb, KERNEL, grid, block, stream, args)                      \
+  switch (vb) {                                                                     \
+    case 16: hipLaunchKernelGGL(KERNEL<16>, grid, block, 0, stream, args); break;  \
+    case 8: hipLaunchKernelGGL(KERNEL<8>, grid, block, 0, stream, args); break;    \
+    case 4: hipLaunchKernelGGL(KERNEL<4>, grid, block, 0, stream, args); break;    \
+    case 2: hipLaunchKernelGGL(KERNEL<2>, grid, block, 0, stream, args); break;    \
+    default: hipLaunchKernelGGL(KERNEL<1>, grid, block, 0, stream, args); break;   \
+  }
 
 template <typename T, int VEC>
 struct Vec {

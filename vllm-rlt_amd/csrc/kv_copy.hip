@@ -6,7 +6,10 @@
 // widest vector (16, 8, 4, 2 or 1 bytes) that every pointer and stride allows.
 //
 // Reference behaviour:
-//   copy_blocks    kv_cache_manager.py:481-523 (page-by-page snapshot/restore)
+//   copy_blocks    on-device block copy (copy-on-write / compaction)
+//   blocks_to_host / blocks_from_host
+//                  kv_cache_manager.py:481-523 (snapshot/restore: the page
+//                  copies to and from host memory, batched into one launch)
 //   finalize       kernels/routing.py:147-177 (finalize_kernel), launched as in
 //                  worker/model_runner.py:1331-1346
 //   finalize_token kv_cache_manager.py:806-831
@@ -17,19 +20,6 @@
 
 namespace vrh {
 namespace {
-
-template <int VB>
-using raw_of = typename RawVec<VB>::type;
-
-int pick_vb(std::initializer_list<int64_t> values, std::initializer_list<const void*> ptrs) {
-  for (int vb = 16; vb > 1; vb >>= 1) {
-    bool ok = true;
-    for (int64_t s : values) ok = ok && (s % vb == 0);
-    for (const void* p : ptrs) ok = ok && ((uintptr_t)p % vb == 0);
-    if (ok) return vb;
-  }
-  return 1;
-}
 
 // ------------------------------------------------------------ block copy
 // grid.x tiles one block (kUnroll * 256 vectors per workgroup), grid.y = pair.
@@ -163,16 +153,114 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
       reinterpret_cast<const raw_t*>(a.vc + src)[j];
 }
 
-#define VRH_DISPATCH_VB(vb, KERNEL, grid, block, stream, args)                      \
-  switch (vb) {                                                                     \
-    case 16: hipLaunchKernelGGL(KERNEL<16>, grid, block, 0, stream, args); break;  \
-    case 8: hipLaunchKernelGGL(KERNEL<8>, grid, block, 0, stream, args); break;    \
-    case 4: hipLaunchKernelGGL(KERNEL<4>, grid, block, 0, stream, args); break;    \
-    case 2: hipLaunchKernelGGL(KERNEL<2>, grid, block, 0, stream, args); break;    \
-    default: hipLaunchKernelGGL(KERNEL<1>, grid, block, 0, stream, args); break;   \
-  }
-
 constexpr int64_t kMaxGridY = 65535;
+
+// ------------------------------------------------- host offload (snapshot)
+// Whole blocks between the pool and pinned host rows (row i <-> blocks[i]),
+// read or written by the kernel through the host memory's device mapping: one
+// launch per direction and no device staging buffer. grid.x tiles a block
+// (kCopyUnroll * 256 vectors per workgroup, all loads issued before the
+// stores to keep many host-link transfers in flight), grid.y = block.
+struct HostCopyArgs {
+  char* kc;
+  char* vc;
+  char* hk;  // device address of the pinned host rows
+  char* hv;
+  const int64_t* blocks;
+  int64_t block_stride;  // bytes between pool blocks
+  int64_t block_bytes;   // bytes per block = bytes per host row
+  int64_t vecs;
+  int64_t base;
+};
+
+template <int VB, bool TO_HOST>
+__device__ __forceinline__ void host_copy_body(const HostCopyArgs& a) {
+  using raw_t = raw_of<VB>;
+  const int64_t row = a.base + blockIdx.y;
+  const int64_t pool_off = a.blocks[row] * a.block_stride;
+  const int64_t host_off = row * a.block_bytes;
+  const raw_t* ks = reinterpret_cast<const raw_t*>((TO_HOST ? a.kc + pool_off : a.hk + host_off));
+  const raw_t* vs = reinterpret_cast<const raw_t*>((TO_HOST ? a.vc + pool_off : a.hv + host_off));
+  raw_t* kd = reinterpret_cast<raw_t*>(TO_HOST ? a.hk + host_off : a.kc + pool_off);
+  raw_t* vd = reinterpret_cast<raw_t*>(TO_HOST ? a.hv + host_off : a.vc + pool_off);
+  const int64_t first = (int64_t)blockIdx.x * (256 * kCopyUnroll) + threadIdx.x;
+  raw_t kr[kCopyUnroll], vr[kCopyUnroll];
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u) {
+    const int64_t i = first + u * 256;
+    if (i < a.vecs) {
+      kr[u] = __builtin_nontemporal_load(ks + i);
+      vr[u] = __builtin_nontemporal_load(vs + i);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u) {
+    const int64_t i = first + u * 256;
+    if (i < a.vecs) {
+      __builtin_nontemporal_store(kr[u], kd + i);
+      __builtin_nontemporal_store(vr[u], vd + i);
+    }
+  }
+}
+
+template <int VB>
+__global__ __launch_bounds__(256) void blocks_to_host_kernel(HostCopyArgs a) {
+  host_copy_body<VB, true>(a);
+}
+template <int VB>
+__global__ __launch_bounds__(256) void blocks_from_host_kernel(HostCopyArgs a) {
+  host_copy_body<VB, false>(a);
+}
+
+// Device address of pinned host memory; null if `p` is not host memory that
+// the runtime mapped for the device (pageable memory must never reach a
+// kernel).
+void* host_device_pointer(void* p) {
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (attr.type != hipMemoryTypeHost) return nullptr;
+  void* d = nullptr;
+  if (hipHostGetDevicePointer(&d, p, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return d;
+}
+
+int host_copy(bool to_host, void* key_cache, void* value_cache, int64_t block_stride_bytes,
+              int64_t block_bytes, const int64_t* blocks, void* host_keys, void* host_values,
+              int64_t n, hipStream_t s, const char* who) {
+  VRH_CHECK_ARG(n >= 0 && block_bytes >= 0 && block_stride_bytes >= block_bytes,
+                "%s: bad sizes n=%lld block_bytes=%lld stride=%lld", who, (long long)n,
+                (long long)block_bytes, (long long)block_stride_bytes);
+  if (n == 0 || block_bytes == 0) return VRH_OK;
+  VRH_CHECK_ARG(key_cache && value_cache && blocks && host_keys && host_values,
+                "%s: null pointer", who);
+  HostCopyArgs a;
+  a.kc = static_cast<char*>(key_cache);
+  a.vc = static_cast<char*>(value_cache);
+  a.hk = static_cast<char*>(host_device_pointer(host_keys));
+  a.hv = static_cast<char*>(host_device_pointer(host_values));
+  VRH_CHECK_ARG(a.hk && a.hv, "%s: host buffers must be pinned host memory (hipHostMalloc)", who);
+  a.blocks = blocks;
+  a.block_stride = block_stride_bytes;
+  a.block_bytes = block_bytes;
+  const int vb = pick_vb({block_stride_bytes, block_bytes},
+                         {key_cache, value_cache, (const void*)a.hk, (const void*)a.hv});
+  a.vecs = block_bytes / vb;
+  const int64_t gx = ceil_div64(a.vecs, 256 * kCopyUnroll);
+  VRH_CHECK_ARG(gx < (1ll << 31), "%s: block too large", who);
+  for (int64_t first = 0; first < n; first += kMaxGridY) {
+    a.base = first;
+    const dim3 grid((unsigned)gx, (unsigned)std::min(n - first, kMaxGridY));
+    if (to_host) VRH_DISPATCH_VB(vb, blocks_to_host_kernel, grid, dim3(256), s, a)
+    else VRH_DISPATCH_VB(vb, blocks_from_host_kernel, grid, dim3(256), s, a)
+  }
+  VRH_RETURN_LAUNCH(who);
+}
 
 }  // namespace
 }  // namespace vrh
@@ -320,4 +408,22 @@ extern "C" int vrh_kv_gather(void* out_k, void* out_v, const void* key_cache,
     VRH_DISPATCH_VB(vb, gather_kernel, grid, dim3(256), s, a);
   }
   VRH_RETURN_LAUNCH("vrh_kv_gather");
+}
+
+extern "C" int vrh_kv_blocks_to_host(const void* key_cache, const void* value_cache,
+                                     int64_t block_stride_bytes, int64_t block_bytes,
+                                     const int64_t* blocks, void* host_keys, void* host_values,
+                                     int64_t n, vrh_stream_t stream) {
+  return host_copy(true, const_cast<void*>(key_cache), const_cast<void*>(value_cache),
+                   block_stride_bytes, block_bytes, blocks, host_keys, host_values, n,
+                   (hipStream_t)stream, "vrh_kv_blocks_to_host");
+}
+
+extern "C" int vrh_kv_blocks_from_host(void* key_cache, void* value_cache,
+                                       int64_t block_stride_bytes, int64_t block_bytes,
+                                       const int64_t* blocks, const void* host_keys,
+                                       const void* host_values, int64_t n, vrh_stream_t stream) {
+  return host_copy(false, key_cache, value_cache, block_stride_bytes, block_bytes, blocks,
+                   const_cast<void*>(host_keys), const_cast<void*>(host_values), n,
+                   (hipStream_t)stream, "vrh_kv_blocks_from_host");
 }

@@ -554,23 +554,35 @@ class KVCacheManager:
         hip.kv_copy_blocks(self.key_cache, self.value_cache, index[:n], index[n:])
 
     def snapshot(self, request_id: str) -> KVSnapshot:
-        """Copy a request's pages and written state to the host, page by page."""
+        """Copy a request's pages and written state to the host.
+
+        Reference: core/kv_cache_manager.py:481-502. Instead of one copy per
+        page, a single kernel writes every page straight into pinned host rows
+        (no device staging buffer, the reference's reason for copying page by
+        page). Returns once the host rows are complete.
+        """
         allocation = self._get_allocation(request_id)
         blocks = [b for table in allocation.block_tables for b in table]
-        pinned = self.device.type == "cuda"
+        if self.device.type != "cuda":
+            raise ValueError("snapshot of the hip build needs a ROCm device pool")
         keys = torch.empty((len(blocks), *self.key_cache.shape[1:]), dtype=self.dtype,
-                           pin_memory=pinned)
-        values = torch.empty_like(keys, pin_memory=pinned)
-        for row, block in enumerate(blocks):
-            keys[row].copy_(self.key_cache[block], non_blocking=True)
-            values[row].copy_(self.value_cache[block], non_blocking=True)
-        if pinned:
-            torch.cuda.current_stream(self.device).synchronize()
+                           pin_memory=True)
+        values = torch.empty_like(keys, pin_memory=True)
+        index = torch.tensor(blocks, dtype=torch.int64).to(self.device)
+        hip.kv_blocks_to_host(self.key_cache, self.value_cache, index, keys, values)
+        torch.cuda.current_stream(self.device).synchronize()
         return KVSnapshot(allocation.max_tokens, len(allocation.block_tables[0]),
                           deepcopy(allocation.written), keys, values)
 
     def restore(self, request_id: str, snapshot: KVSnapshot) -> None:
-        """Load a snapshot into a fresh allocation of the same size."""
+        """Load a snapshot into a fresh allocation of the same size.
+
+        Reference: core/kv_cache_manager.py:504-523. One kernel reads the
+        snapshot's host rows into the new blocks on the current stream; the
+        call returns after that stream has finished with the host rows, so the
+        caller may drop the snapshot immediately (the reference's host copies
+        are blocking too).
+        """
         allocation = self._get_allocation(request_id)
         if allocation.max_tokens != snapshot.max_tokens:
             raise ValueError("snapshot capacity does not match the allocation")
@@ -579,7 +591,12 @@ class KVCacheManager:
         if any(w.prefix or w.pending for plane in allocation.written for w in plane):
             raise RuntimeError("cannot restore into an allocation that already holds KV")
         blocks = [b for table in allocation.block_tables for b in table]
-        for row, block in enumerate(blocks):
-            self.key_cache[block].copy_(snapshot.keys[row], non_blocking=True)
-            self.value_cache[block].copy_(snapshot.values[row], non_blocking=True)
+        if self.device.type != "cuda":
+            raise ValueError("restore of the hip build needs a ROCm device pool")
+        keys, values = snapshot.keys, snapshot.values
+        if not keys.is_pinned():
+            keys, values = keys.pin_memory(), values.pin_memory()
+        index = torch.tensor(blocks, dtype=torch.int64).to(self.device)
+        hip.kv_blocks_from_host(self.key_cache, self.value_cache, index, keys, values)
+        torch.cuda.current_stream(self.device).synchronize()
         allocation.written = deepcopy(snapshot.written)

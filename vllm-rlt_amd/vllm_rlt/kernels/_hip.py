@@ -19,7 +19,7 @@ from functools import cache
 LIBRARY_NAME = "libvllm_rlt_hip.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "_lib",
                             LIBRARY_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 VRH_DTYPE_F32, VRH_DTYPE_F16, VRH_DTYPE_BF16 = 0, 1, 2
 
@@ -63,6 +63,13 @@ SIGNATURES: dict[str, tuple[object, list]] = {
         _INT, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _I32, _P]
     ),
     "vrh_routing_slots": (_INT, [_P, _P, _I64, _I64, _P]),
+    "vrh_kv_blocks_to_host": (_INT, [_P, _P, _I64, _I64, _P, _P, _P, _I64, _P]),
+    "vrh_kv_blocks_from_host": (_INT, [_P, _P, _I64, _I64, _P, _P, _P, _I64, _P]),
+    "vrh_gather_rows": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
+    "vrh_scatter_rows": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "vrh_gather_segments": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "vrh_scatter_segments": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "vrh_silu_and_mul": (_INT, [_INT, _P, _P, _P, _I64, _P]),
 }
 
 

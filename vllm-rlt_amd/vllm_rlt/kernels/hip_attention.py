@@ -15,7 +15,9 @@ Reference operator contracts mirrored here:
   kv_gather                   core/kv_cache_manager.py:834-854
   kv_finalize                 kernels/routing.py:147-177 + worker/model_runner.py:1331-1346
   kv_finalize_token           core/kv_cache_manager.py:806-831
-  kv_copy_blocks              core/kv_cache_manager.py:481-523 (device part)
+  kv_copy_blocks              on-device block copy (copy-on-write; no reference counterpart)
+  kv_blocks_to_host / kv_blocks_from_host
+                              core/kv_cache_manager.py:481-523 (snapshot/restore copies)
   expand_kv_addresses         kernels/metadata.py:7-24
   routing_metadata / slots    kernels/routing.py:7-48
 """
@@ -383,6 +385,62 @@ def kv_copy_blocks(key_cache, value_cache, src_blocks, dst_blocks):
             _stream(key_cache),
         ),
         "vrh_kv_copy_blocks",
+    )
+
+
+def _offload_args(key_cache, value_cache, blocks, host_keys, host_values):
+    device = key_cache.device
+    _on_gpu("key_cache", key_cache, device)
+    if key_cache.shape != value_cache.shape or key_cache.stride() != value_cache.stride():
+        raise ValueError("key_cache and value_cache must match")
+    _check_int("blocks", blocks, torch.int64, 1, device)
+    block = key_cache[0]
+    if not block.is_contiguous():
+        raise ValueError("each pool block must be contiguous")
+    shape = (blocks.shape[0], *key_cache.shape[1:])
+    for name, host in (("host_keys", host_keys), ("host_values", host_values)):
+        if host.device.type != "cpu" or not host.is_pinned():
+            raise ValueError(f"{name} must be a pinned host tensor (pin_memory=True)")
+        if tuple(host.shape) != shape or host.dtype != key_cache.dtype or not host.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {key_cache.dtype} tensor of shape "
+                             f"{list(shape)}")
+    es = key_cache.element_size()
+    return key_cache.stride(0) * es, block.numel() * es
+
+
+def kv_blocks_to_host(key_cache, value_cache, blocks, host_keys, host_values):
+    """Row i of the pinned host tensors = block blocks[i] of each pool (all layers):
+    the snapshot copies of core/kv_cache_manager.py:481-502 in one launch. The rows
+    are complete once the current stream has passed this call."""
+    stride, nbytes = _offload_args(key_cache, value_cache, blocks, host_keys, host_values)
+    if blocks.shape[0] == 0:
+        return
+    lib = library()
+    lib.check(
+        lib.vrh_kv_blocks_to_host(
+            key_cache.data_ptr(), value_cache.data_ptr(), stride, nbytes,
+            blocks.contiguous().data_ptr(), host_keys.data_ptr(), host_values.data_ptr(),
+            blocks.shape[0], _stream(key_cache),
+        ),
+        "vrh_kv_blocks_to_host",
+    )
+
+
+def kv_blocks_from_host(key_cache, value_cache, blocks, host_keys, host_values):
+    """Block blocks[i] of each pool = row i of the pinned host tensors: the restore
+    copies of core/kv_cache_manager.py:504-523 in one launch. The host rows must
+    stay alive until the current stream has passed this call."""
+    stride, nbytes = _offload_args(key_cache, value_cache, blocks, host_keys, host_values)
+    if blocks.shape[0] == 0:
+        return
+    lib = library()
+    lib.check(
+        lib.vrh_kv_blocks_from_host(
+            key_cache.data_ptr(), value_cache.data_ptr(), stride, nbytes,
+            blocks.contiguous().data_ptr(), host_keys.data_ptr(), host_values.data_ptr(),
+            blocks.shape[0], _stream(key_cache),
+        ),
+        "vrh_kv_blocks_from_host",
     )
 
 
