@@ -164,6 +164,82 @@ def cpu_baseline(work, budget_s):
     }
 
 
+def mlp_and_rows_extras(device, chunk_rows):
+    """SiLU-and-Mul at the Ouro-1.4B MLP width and the WCPB hidden-state segment
+    gather/scatter of the config-4 chunks (HBM-bound byte movers)."""
+    import torch
+
+    from vllm_rlt.kernels.activation import silu_and_mul
+    from vllm_rlt.kernels.routing import gather_segments, scatter_segments
+
+    out = {}
+    gen = torch.Generator().manual_seed(1)
+    inter = 5632
+    for name, tokens, offset in (("silu_and_mul_prefill_8192x5632", 8192, 0),
+                                 ("silu_and_mul_prefill_8192x5632_misaligned", 8192, 1),
+                                 ("silu_and_mul_decode_64x5632", 64, 0)):
+        count = tokens * inter
+        gate = torch.randn(count + offset, generator=gen).to(torch.bfloat16).to(device)[offset:]
+        up = torch.randn(count + offset, generator=gen).to(torch.bfloat16).to(device)[offset:]
+        ms = graph_time_ms([lambda g=gate, u=up: silu_and_mul(g, u)] * 8)
+        nbytes = count * 2 * 3
+        out[name] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 2), "us": round(ms * 1e3, 2),
+                     "pct_of_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+        del gate, up
+    hidden = 2048
+    slots, pool_rows = 64, 1024
+    pool = torch.randn(slots * pool_rows, hidden, generator=gen).to(torch.bfloat16).to(device)
+    seg = [[(7 * i) % slots, 512 * (i % 2), 512, 512 * i, 1] for i in range(chunk_rows // 512)]
+    segments = torch.tensor(seg, dtype=torch.int64, device=device)
+    batch = torch.empty(chunk_rows, hidden, dtype=torch.bfloat16, device=device)
+    g_ms = graph_time_ms([lambda: gather_segments(pool, segments, batch, pool_rows, 512)] * 16)
+    s_ms = graph_time_ms([lambda: scatter_segments(batch, segments, pool, pool_rows, 512)] * 16)
+    nbytes = chunk_rows * hidden * 2 * 2
+    for name, ms in (("gather_segments_config4", g_ms), ("scatter_segments_config4", s_ms)):
+        out[name] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 2), "us": round(ms * 1e3, 2),
+                     "rows": chunk_rows}
+    return out
+
+
+def offload_extras(device):
+    """Preemption snapshot/restore of a 4096-token Ouro-1.4B request (256 pages of
+    3 MiB, K + V) through pinned host memory: one launch per direction, against
+    the reference's one copy per page. Host-link bound (PCIe 5.0 x16: 64 GB/s)."""
+    import torch
+
+    from vllm_rlt.kernels.hip_attention import kv_blocks_from_host, kv_blocks_to_host
+
+    pages = 256
+    shape = (pages + 64, 24, 16, 16, 128)
+    key_pool = torch.randn(shape[1:], dtype=torch.bfloat16, device=device).expand(shape).clone()
+    value_pool = key_pool.clone()
+    blocks = torch.randperm(pages + 64)[:pages]
+    index = blocks.to(device)
+    host_k = torch.empty((pages, *shape[1:]), dtype=torch.bfloat16, pin_memory=True)
+    host_v = torch.empty_like(host_k, pin_memory=True)
+    nbytes = 2 * host_k.numel() * 2
+    kv_blocks_to_host(key_pool, value_pool, index, host_k, host_v)
+    torch.cuda.synchronize()
+    to_ms = event_time_ms(lambda: kv_blocks_to_host(key_pool, value_pool, index, host_k, host_v), 3)
+    from_ms = event_time_ms(
+        lambda: kv_blocks_from_host(key_pool, value_pool, index, host_k, host_v), 3)
+
+    def per_page():
+        for row, block in enumerate(blocks.tolist()):
+            host_k[row].copy_(key_pool[block], non_blocking=True)
+            host_v[row].copy_(value_pool[block], non_blocking=True)
+
+    per_page()
+    torch.cuda.synchronize()
+    page_ms = event_time_ms(per_page, 2)
+    return {"snapshot_256_pages_batched": {"gbs": round(nbytes / (to_ms * 1e-3) / 1e9, 2),
+                                           "ms": round(to_ms, 3), "bytes": nbytes},
+            "restore_256_pages_batched": {"gbs": round(nbytes / (from_ms * 1e-3) / 1e9, 2),
+                                          "ms": round(from_ms, 3)},
+            "snapshot_256_pages_per_page_copies": {
+                "gbs": round(nbytes / (page_ms * 1e-3) / 1e9, 2), "ms": round(page_ms, 3)}}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -331,10 +407,22 @@ def main():
             "us": round(append_ms * 1e3, 2), "rows": int(pw.k_new.shape[0]),
             "pct_of_hbm_peak": round(100 * pw.append_bytes() / (append_ms * 1e-3) / 1e9
                                      / HBM_PEAK_GBS, 2)}
+        prefill_graph_ms = graph_time_ms(
+            [lambda: paged_prefill_attention(pw.q, kc, vc, pw.block_tables, pw.context_lengths,
+                                             pw.cu_seqlens_q, pw.max_seqlen_q)] * 4, replays=3)
         extras["prefill_config4"] = {
             "tflops": round(flops / (prefill_ms * 1e-3) / 1e12, 2), "ms": round(prefill_ms, 4),
             "pct_of_bf16_mfma_peak": round(100 * flops / (prefill_ms * 1e-3) / 1e12
-                                           / BF16_PEAK_TFLOPS, 2)}
+                                           / BF16_PEAK_TFLOPS, 2),
+            "graph_ms": round(prefill_graph_ms, 4),
+            "graph_tflops": round(flops / (prefill_graph_ms * 1e-3) / 1e12, 2)}
+        # Hidden-state segments of the config-4 chunks around prefill: gather the
+        # 16 x 512 chunk rows (Ouro hidden 2048, bf16) from the state pool.
+        chunk_rows = pw.chunk_sequences * 512
+        del pw, kc, vc
+        torch.cuda.empty_cache()
+        extras.update(mlp_and_rows_extras(device, chunk_rows))
+        extras.update(offload_extras(device))
         result["extras"] = extras
     print(json.dumps(result), flush=True)
 

@@ -240,6 +240,25 @@ def test_packed_prefill_mixed_with_decode_rows(gpu):
     tables = tables.to(gpu)
     actual = paged_prefill_attention(q, k, v, tables, lengths, cu, 512)
     assert_close(actual, oracle_prefill(q, k, v, tables, lengths, cu), torch.bfloat16)
+    # The decode rows run on a side stream forked from and joined back into the
+    # current stream: a captured graph must reproduce the eager result on every
+    # replay, with other eager work and synchronisations in between.
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        paged_prefill_attention(q, k, v, tables, lengths, cu, 512)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        captured = paged_prefill_attention(q, k, v, tables, lengths, cu, 512)
+    for _ in range(3):
+        captured.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, actual)
+        paged_prefill_attention(q, k, v, tables, lengths, cu, 512)  # eager work in between
 
 
 def test_empty_inputs(gpu):
