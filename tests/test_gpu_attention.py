@@ -217,6 +217,35 @@ def test_packed_prefill_matches_per_query_oracle(gpu, dtype, head_dim, heads, kv
     assert_close(actual, oracle_prefill(q, k, v, tables, lengths, cu), dtype)
 
 
+@pytest.mark.parametrize("block", [2, 5, 8, 32, 64])
+@pytest.mark.parametrize("dtype,head_dim,heads,kv_heads", [(torch.bfloat16, 128, 4, 4),
+                                                          (torch.float16, 64, 4, 2)])
+def test_packed_prefill_block_sizes_and_long_tables(gpu, block, dtype, head_dim, heads, kv_heads):
+    """MFMA tiles with every page-addressing path (power-of-two pages smaller and
+    larger than a staging store's rows, non-power-of-two pages) and page tables
+    longer than the 512-entry LDS segment (9000 keys: 141 to 4500 pages)."""
+    from vllm_rlt.kernels.hip_attention import paged_prefill_attention
+
+    sequences = [(9000, 130), (700, 300), (33, 33), (513, 1)]
+    gen = torch.Generator().manual_seed(block)
+    pages = sum(-(-n // block) for n, _ in sequences)
+    k = torch.randn(pages, block, kv_heads, head_dim, generator=gen).to(dtype).to(gpu)
+    v = torch.randn(pages, block, kv_heads, head_dim, generator=gen).to(dtype).to(gpu)
+    order = torch.randperm(pages, generator=gen).tolist()
+    width = max(-(-n // block) for n, _ in sequences)
+    tables = torch.full((len(sequences), width), -1, dtype=torch.int32)
+    for s, (n, _) in enumerate(sequences):
+        ids = [order.pop() for _ in range(-(-n // block))]
+        tables[s, : len(ids)] = torch.tensor(ids, dtype=torch.int32)
+    total = sum(c for _, c in sequences)
+    q = torch.randn(total, heads, head_dim, generator=gen).to(dtype).to(gpu)
+    cu = torch.tensor(np.cumsum([0] + [c for _, c in sequences]), dtype=torch.int32, device=gpu)
+    lengths = torch.tensor([n for n, _ in sequences], dtype=torch.int32, device=gpu)
+    tables = tables.to(gpu)
+    actual = paged_prefill_attention(q, k, v, tables, lengths, cu, 300)
+    assert_close(actual, oracle_prefill(q, k, v, tables, lengths, cu), dtype)
+
+
 def test_packed_prefill_mixed_with_decode_rows(gpu):
     """WCPB shape in miniature: long chunks with prefixes and q_len = 1 rows."""
     from vllm_rlt.kernels.hip_attention import paged_prefill_attention
