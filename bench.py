@@ -55,6 +55,8 @@ def parse_args():
                         help="only the decode step (no append/prefill/cpu legs)")
     parser.add_argument("--cpu-seconds", type=float, default=10.0,
                         help="budget of the CPU baseline sample")
+    parser.add_argument("--leg", choices=["prefill_config4", "prefill_chunks_config4"],
+                        help="run only this workload (for profiling) and print its timing")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run vrh_kv_copy_blocks over a known byte count (the "
                              "reference kernel for scaling rocprof FETCH_SIZE/WRITE_SIZE)")
@@ -240,6 +242,27 @@ def offload_extras(device):
                 "gbs": round(nbytes / (page_ms * 1e-3) / 1e9, 2), "ms": round(page_ms, 3)}}
 
 
+def single_leg(name, repeats):
+    """One workload alone, for rocprofv3 runs: config-4 packed prefill with its
+    decode rows, or its 16 chunks only."""
+    import torch
+
+    from vllm_rlt import workloads
+    from vllm_rlt.kernels.hip_attention import paged_prefill_attention
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    kw = {"decode_rows": 0} if name == "prefill_chunks_config4" else {}
+    pw = workloads.config4(device=device, **kw)
+    kc, vc = pw.key_cache[:, 0], pw.value_cache[:, 0]
+    ms = event_time_ms(lambda: paged_prefill_attention(pw.q, kc, vc, pw.block_tables,
+                                                       pw.context_lengths, pw.cu_seqlens_q,
+                                                       pw.max_seqlen_q), repeats)
+    flops = pw.flops()
+    print(json.dumps({"leg": name, "ms": round(ms, 4),
+                      "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "flops": flops}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -248,6 +271,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.leg:
+        single_leg(args.leg, args.steps)
         return
     import torch
 
