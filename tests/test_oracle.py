@@ -273,3 +273,18 @@ def test_row_and_segment_oracle_literal_vectors():
     ref.scatter_segments(batch, segments, back, 4)
     assert back[5].tolist() == [15, 16, 17] and back[6].tolist() == [18, 19, 20]
     assert back[3].tolist() == [0, 0, 0]  # keep = 0: not stored
+
+
+def test_torch_cpu_restatement_matches_numpy_oracle():
+    # the CPU baseline's Torch restatement must compute the oracle's function
+    from oracle import torch_ref
+
+    gen = torch.Generator().manual_seed(4)
+    kc = torch.randn(12, 4, 2, 8, generator=gen)
+    vc = torch.randn(12, 4, 2, 8, generator=gen)
+    q = torch.randn(3, 4, 8, generator=gen)
+    tables = torch.tensor([[5, 1, 9], [0, 0, 0], [11, 3, 7]], dtype=torch.int32)
+    lengths = torch.tensor([10, 0, 12], dtype=torch.int32)
+    got = torch_ref.paged_attention(q, kc, vc, tables, lengths)
+    want = ref.paged_attention(q.numpy(), kc.numpy(), vc.numpy(), tables.numpy(), lengths.numpy())
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-5, atol=1e-6)
