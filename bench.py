@@ -51,6 +51,8 @@ def parse_args():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--eager", action="store_true",
+                        help="time the decode step as eager launches instead of a HIP graph")
     parser.add_argument("--skip-extras", action="store_true",
                         help="only the decode step (no append/prefill/cpu legs)")
     parser.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -321,9 +323,26 @@ def main():
     vviews = [work.value_cache[:, layer] for layer in range(layers)]
     tables, lengths, q = work.block_tables, work.context_lengths, work.q
 
-    def step():
+    def eager_step():
         for layer in range(layers):
             paged_attention(q, kviews[layer], vviews[layer], tables, lengths)
+
+    # The reference runs decode steps under CUDA graphs (worker/cuda_graph.py);
+    # one step = one replay of the 24 captured layer calls (same kernels and
+    # bytes as the eager loop, without per-launch host gaps). --eager times
+    # the eager loop instead.
+    step = eager_step
+    if not args.eager:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            eager_step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            eager_step()
+        step = graph.replay
 
     for _ in range(args.warmup):
         step()
@@ -368,6 +387,7 @@ def main():
             "decode_bytes_per_layer_call": decode_bytes,
             "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
             "tokens_per_s": round(work.rows * layers / (wall / args.steps), 1),
+            "step": "eager launches" if args.eager else "HIP graph replay of the 24 layer calls",
         },
         "roofline": {
             "bound": "hbm",
