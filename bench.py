@@ -229,6 +229,59 @@ def mlp_and_rows_extras(device, chunk_rows):
     return out
 
 
+def metadata_extras(device):
+    """The integer routing / address kernels at decode and WCPB sizes (latency:
+    microseconds per call, graph-timed) and the ``read`` gather of one
+    4096-token request (bytes read + written)."""
+    import torch
+
+    from vllm_rlt.kernels.hip_attention import (
+        expand_kv_addresses,
+        kv_gather,
+        routing_metadata,
+        routing_slots,
+    )
+
+    gen = torch.Generator().manual_seed(3)
+    out = {}
+    # async routing of a 64-row decode batch: 64 slots x 4 planes, 257-page tables
+    rows, planes, width, page = 64, 4, 257, 16
+    tables = torch.randint(0, 40000, (rows * planes, width), generator=gen,
+                           dtype=torch.int32).to(device)
+    desc = torch.stack([torch.randperm(rows, generator=gen), torch.randint(0, planes, (rows,),
+                        generator=gen), torch.randint(0, width * page, (rows,), generator=gen)],
+                       1).to(torch.int64).to(device)
+    i64 = lambda: torch.empty(rows, dtype=torch.int64, device=device)
+    slots, positions, blocks, offsets = i64(), i64(), i64(), i64()
+    lengths = torch.empty(rows, dtype=torch.int32, device=device)
+    out_tables = torch.empty((rows, width), dtype=torch.int32, device=device)
+    meta_ms = graph_time_ms([lambda: routing_metadata(
+        desc, tables, n=rows, size=rows, width=width, page=page, planes=planes,
+        out_width=width, slots=slots, positions=positions, lengths=lengths, blocks=blocks,
+        offsets=offsets, out_tables=out_tables)] * 32)
+    slots_ms = graph_time_ms([lambda: routing_slots(desc, slots, rows, rows)] * 32)
+    # WCPB write addresses of the config-4 batch size
+    n = 8039
+    pos = torch.randint(0, 8192, (n,), generator=gen, dtype=torch.int64).to(device)
+    seqs = torch.randint(0, 64, (n,), generator=gen, dtype=torch.int32).to(device)
+    tab = torch.randint(0, 40000, (64, 513), generator=gen, dtype=torch.int32).to(device)
+    b8, o8 = torch.empty(n, dtype=torch.int64, device=device), torch.empty(n, dtype=torch.int64,
+                                                                            device=device)
+    expand_ms = graph_time_ms([lambda: expand_kv_addresses(pos, seqs, tab, 16, b8, o8)] * 32)
+    out["routing_metadata_64_rows_us"] = round(meta_ms * 1e3, 2)
+    out["routing_slots_64_rows_us"] = round(slots_ms * 1e3, 2)
+    out["expand_kv_addresses_8039_us"] = round(expand_ms * 1e3, 2)
+    # read (kv_gather) of a 4096-token request from a 24-layer pool layer view
+    pool = torch.randn((300, 24, 16, 16, 128), generator=gen).to(torch.bfloat16).to(device)
+    table = torch.randperm(300, generator=gen)[:256].to(torch.int32).to(device)
+    kview, vview = pool[:, 5], pool[:, 7]
+    gather_ms = graph_time_ms([lambda: kv_gather(kview, vview, table, 4096)] * 8)
+    gbytes = 4096 * 16 * 128 * 2 * 2 * 2
+    out["kv_gather_4096_tokens"] = {"gbs": round(gbytes / (gather_ms * 1e-3) / 1e9, 2),
+                                    "us": round(gather_ms * 1e3, 2)}
+    return out
+
+
 def offload_extras(device):
     """Preemption snapshot/restore of a 4096-token Ouro-1.4B request (256 pages of
     3 MiB, K + V) through pinned host memory: one launch per direction, against
@@ -492,6 +545,7 @@ def main():
         del pw, kc, vc
         torch.cuda.empty_cache()
         extras.update(mlp_and_rows_extras(device, chunk_rows))
+        extras.update(metadata_extras(device))
         extras.update(offload_extras(device))
         result["extras"] = extras
     print(json.dumps(result), flush=True)
