@@ -153,3 +153,41 @@ def test_library_rejects_bad_arguments_without_a_gpu():
     assert code == 1 and b"destination" in lib.vrh_last_error()
     # zero-size work is a no-op success
     assert lib.vrh_kv_copy_blocks(1, 1, 64, 64, 1, 1, 0, None) == 0
+
+
+def test_silu_and_mul_argument_contract_on_cpu():
+    # reference tests/test_activation.py:79-95: checks precede any device work
+    from vllm_rlt.kernels.activation import silu_and_mul
+
+    with pytest.raises(ValueError, match="same shape"):
+        silu_and_mul(torch.ones(2, 7), torch.ones(1, 7))
+    with pytest.raises(TypeError, match="same dtype"):
+        silu_and_mul(torch.ones(7), torch.ones(7, dtype=torch.float16))
+    for dtype in (torch.int32, torch.float64):
+        with pytest.raises(TypeError, match="supports float32"):
+            silu_and_mul(torch.ones(7, dtype=dtype), torch.ones(7, dtype=dtype))
+    # no CPU path in the hip build
+    with pytest.raises(ValueError, match="ROCm"):
+        silu_and_mul(torch.ones(7), torch.ones(7))
+
+
+def test_row_movers_reject_host_tensors_and_bad_shapes():
+    from vllm_rlt.kernels import routing
+
+    pool, out = torch.zeros(4, 8), torch.zeros(2, 8)
+    with pytest.raises(ValueError, match="ROCm"):
+        routing.gather_rows(pool, torch.zeros(2, dtype=torch.int64), out, 2)
+    with pytest.raises(ValueError, match="ROCm"):
+        routing.gather_segments(pool, torch.zeros(1, 5, dtype=torch.int64), out, 2, 2)
+
+
+def test_silu_and_mul_abi_rejects_bad_arguments_without_a_gpu():
+    lib = _hip.library()
+    assert lib.vrh_silu_and_mul(7, 16, 16, 16, 4, None) == 1
+    assert b"supports float32" in lib.vrh_last_error()
+    assert lib.vrh_silu_and_mul(2, 16, 16, 16, -1, None) == 1
+    assert lib.vrh_silu_and_mul(2, 0, 16, 16, 0, None) == 0          # empty: no launch
+    assert lib.vrh_silu_and_mul(2, 16, 17, 16, 4, None) == 1         # bf16 pointer misaligned
+    assert b"aligned" in lib.vrh_last_error()
+    assert lib.vrh_gather_rows(16, 16, 16, 0, 4, 64, 32, 64, None) == 1  # stride < width
+    assert b"stride" in lib.vrh_last_error()
