@@ -15,6 +15,12 @@
  * Block ids are int32 in tables and int64 in write addresses; every physical
  * offset is computed in 64-bit (pools beyond 2^31 elements).
  *
+ * Index arguments (block ids, write offsets, slots, descriptors) are trusted,
+ * as in the reference's Triton kernels: they are read on the device and not
+ * range-checked there (the host cannot see them without a synchronisation).
+ * An id outside the pool addresses memory outside it. Sizes, strides, dtypes
+ * and pointers are checked on the host before any launch.
+ *
  * Reference interfaces each entry point replaces (paths relative to the
  * vllm-rlt source tree):
  *   vrh_kv_append            kv_cache_manager.py:689-699 (index_put append),

@@ -90,6 +90,11 @@ template <int VB>
 using raw_of = typename RawVec<VB>::type;
 
 // Widest byte-copy vector (16, 8, 4, 2 or 1) dividing every size and pointer.
+// Bytes per element of a storage dtype code (0 for an unknown code).
+inline int dtype_bytes(int dtype) {
+  return dtype == VRH_DTYPE_F32 ? 4 : (dtype == VRH_DTYPE_F16 || dtype == VRH_DTYPE_BF16) ? 2 : 0;
+}
+
 inline int pick_vb(std::initializer_list<int64_t> values, std::initializer_list<const void*> ptrs) {
   for (int vb = 16; vb > 1; vb >>= 1) {
     bool ok = true;

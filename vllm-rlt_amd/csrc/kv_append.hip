@@ -37,7 +37,7 @@ struct AppendArgs {
 
 template <int VECB>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
-  using raw_t = typename RawVec<VECB>::type;
+  using raw_t = raw_of<VECB>;
   const int64_t row = a.row_base + blockIdx.y;  // one job per (row, layer)
   if (a.active != nullptr && row >= (int64_t)(*a.active)) return;
   if (a.mask != nullptr && a.mask[row] == 0) return;
@@ -63,30 +63,10 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   *reinterpret_cast<raw_t*>(a.vc + dst) = vv;
 }
 
-int elem_size(int dtype) {
-  switch (dtype) {
-    case VRH_DTYPE_F32: return 4;
-    case VRH_DTYPE_F16: return 2;
-    case VRH_DTYPE_BF16: return 2;
-    default: return 0;
-  }
-}
-
 }  // namespace
 }  // namespace vrh
 
 using namespace vrh;
-
-static int pick_vec_bytes(int64_t head_bytes, std::initializer_list<int64_t> strides,
-                          std::initializer_list<const void*> ptrs) {
-  for (int vb = 16; vb > 1; vb >>= 1) {
-    bool ok = head_bytes % vb == 0;
-    for (int64_t s : strides) ok = ok && (s % vb == 0);
-    for (const void* p : ptrs) ok = ok && ((uintptr_t)p % vb == 0);
-    if (ok) return vb;
-  }
-  return 1;
-}
 
 extern "C" int vrh_kv_append(int dtype, void* key_cache, void* value_cache,
                              int64_t cache_block_stride, int64_t cache_token_stride,
@@ -98,7 +78,7 @@ extern "C" int vrh_kv_append(int dtype, void* key_cache, void* value_cache,
                              const int64_t* write_offsets, const uint8_t* write_mask,
                              const int32_t* active_rows, int64_t rows, int32_t layers,
                              int32_t kv_heads, int32_t head_dim, vrh_stream_t stream) {
-  const int es = elem_size(dtype);
+  const int es = dtype_bytes(dtype);
   VRH_CHECK_ARG(es > 0, "vrh_kv_append: unknown dtype %d", dtype);
   VRH_CHECK_ARG(rows >= 0 && layers >= 1 && kv_heads >= 1 && head_dim >= 1,
                 "vrh_kv_append: bad sizes rows=%lld layers=%d kv_heads=%d head_dim=%d",
@@ -128,11 +108,9 @@ extern "C" int vrh_kv_append(int dtype, void* key_cache, void* value_cache,
   a.v_layer = v_layer_stride * es;
   a.row_base = 0;
   const int64_t head_bytes = (int64_t)head_dim * es;
-  const int vb = pick_vec_bytes(
-      head_bytes,
-      {a.c_block, a.c_token, a.c_head, a.c_layer, a.k_row, a.k_head, a.k_layer, a.v_row,
-       a.v_head, a.v_layer},
-      {key_cache, value_cache, k, v});
+  const int vb = pick_vb({head_bytes, a.c_block, a.c_token, a.c_head, a.c_layer, a.k_row,
+                          a.k_head, a.k_layer, a.v_row, a.v_head, a.v_layer},
+                         {key_cache, value_cache, k, v});
   a.vecs_per_head = (int32_t)(head_bytes / vb);
   a.vec_shift = -1;
   if ((a.vecs_per_head & (a.vecs_per_head - 1)) == 0) {
@@ -149,18 +127,7 @@ extern "C" int vrh_kv_append(int dtype, void* key_cache, void* value_cache,
     const int64_t count = rows - first < 65535 ? rows - first : 65535;
     part.row_base = first;
     dim3 grid(gx, (unsigned)count, (unsigned)layers);
-    switch (vb) {
-#define VRH_APPEND_CASE(VB)                                                  \
-  case VB:                                                                   \
-    hipLaunchKernelGGL(kv_append_kernel<VB>, grid, dim3(256), 0, s, part); \
-    break;
-      VRH_APPEND_CASE(16)
-      VRH_APPEND_CASE(8)
-      VRH_APPEND_CASE(4)
-      VRH_APPEND_CASE(2)
-      VRH_APPEND_CASE(1)
-#undef VRH_APPEND_CASE
-    }
+    VRH_DISPATCH_VB(vb, kv_append_kernel, grid, dim3(256), s, part)
   }
   VRH_RETURN_LAUNCH("vrh_kv_append");
 }

@@ -406,10 +406,6 @@ bool launch_decode(int vec, int lpt, dim3 grid, dim3 block, hipStream_t s, const
   }
 }
 
-int dtype_size(int dtype) {
-  return dtype == VRH_DTYPE_F32 ? 4 : (dtype == VRH_DTYPE_F16 || dtype == VRH_DTYPE_BF16) ? 2 : 0;
-}
-
 }  // namespace
 }  // namespace vrh
 
@@ -435,7 +431,7 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
                     int64_t k_head_stride, int64_t v_block_stride, int64_t v_token_stride,
                     int64_t v_head_stride, int32_t window, void* workspace,
                     size_t workspace_bytes, hipStream_t s, const char* who) {
-  const int es = dtype_size(dtype);
+  const int es = dtype_bytes(dtype);
   VRH_CHECK_ARG(es > 0, "%s: unknown dtype %d", who, dtype);
   VRH_CHECK_ARG(rows >= 0 && q_heads >= 1 && kv_heads >= 1 && q_heads % kv_heads == 0,
                 "%s: query heads must be a positive multiple of KV heads", who);
