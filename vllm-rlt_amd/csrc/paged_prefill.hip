@@ -383,10 +383,16 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
   // lazy rescale: the reference max (log2 domain, finite from the start)
   // only moves when some lane's max grows by more than 8, so P stays <= 2^8
   // and most sub-blocks skip the O rescale.
-  auto mask_max = [&](int j, f32x16& st) {
+  auto unmasked = [&](int j) {
+    const int k0 = j * kSB;
+    return k0 + kSB <= end && k0 + kSB - 1 <= wave_qpos0;
+  };
+  // This lane's max over sub-block j's scores; with masked_c true the causal
+  // / end mask is first applied to st in place.
+  auto row_max = [&](int j, f32x16& st, auto masked_c) {
     const int k0 = j * kSB;
     float mx = -INFINITY;
-    if (k0 + kSB <= end && k0 + kSB - 1 <= wave_qpos0) {
+    if constexpr (!decltype(masked_c)::value) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, st[e]);
     } else {
@@ -398,6 +404,10 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
         mx = fmaxf(mx, st[e]);
       }
     }
+    return mx;
+  };
+  // Max over the lane pair and the lazy rescale of O and the partial sum.
+  auto rescale = [&](float mx) {
     {
       // Max with lane l ^ 32: one v_permlane32_swap gives both halves.
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
@@ -414,6 +424,10 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
       m = mnew;
     }
   };
+  auto mask_max = [&](int j, f32x16& st) {
+    if (unmasked(j)) rescale(row_max(j, st, std::false_type{}));
+    else rescale(row_max(j, st, std::true_type{}));
+  };
 
   // Pipeline over 32-key sub-blocks, kStages (3 or 4) LDS stages, sub-block
   // j in stage j % kStages. Step j:
@@ -424,7 +438,8 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
   //   j + 3 into the same registers (one step of latency to land);
   //   S1: every LDS operand read (K of j + 1, V of j), then the QK^T MFMAs of
   //       j + 1 interleaved with the probability VALU work of j;
-  //   S2: PV of sub-block j (MFMA), then mask / max / rescale of j + 1.
+  //   S2: PV of sub-block j (MFMA) interleaved with the mask / row max of
+  //       j + 1 (VALU), then the lane-pair max and rescale.
   // The loop is unrolled by kStages so every stage address is a
   // compile-time offset.
   using H0 = std::integral_constant<int, 0>;
@@ -468,9 +483,28 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
           __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        pv(vop, pop);
+        // PV of sub-block j with the row max of j + 1 interleaved.
+        float mx;
         st = st_n;
-        mask_max(j + 1, st);
+        if (unmasked(j + 1)) {
+          pv(vop, pop);
+          mx = row_max(j + 1, st, std::false_type{});
+#pragma unroll
+          for (int i = 0; i < 2 * DB; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+          }
+        } else {
+          pv(vop, pop);
+          mx = row_max(j + 1, st, std::true_type{});
+#pragma unroll
+          for (int i = 0; i < 2 * DB; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        rescale(mx);
       } else {
         probs(st, pop);
         vload(hc, vop);
