@@ -310,7 +310,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
 
 // Log-sum-exp merge of a row's split partials, one wave per (row, q head),
 // 4 waves per workgroup. Lane s holds split s's weight; each lane owns ND
-// dims and issues its partial loads 8 splits at a time, all in flight.
+// dims and issues the loads of all splits at once.
 template <typename T, int ND>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   const int lane = threadIdx.x & 63;
@@ -334,24 +334,21 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   float acc[ND];
 #pragma unroll
   for (int e = 0; e < ND; ++e) acc[e] = 0.f;
-  for (int s0 = 0; s0 < P.nsplit; s0 += 8) {
-    float v[8][ND];
+  // Every split's partial row is loaded at once (they do not depend on the
+  // weights), then combined in split order.
+  float v[kMaxSplits][ND];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < kMaxSplits; ++j)
 #pragma unroll
-      for (int e = 0; e < ND; ++e) {
-        const int d = lane + 64 * e;
-        v[j][e] = (s0 + j < P.nsplit && d < a.head_dim) ? part[(int64_t)(s0 + j) * a.head_dim + d]
-                                                       : 0.f;
-      }
+    for (int e = 0; e < ND; ++e) {
+      const int d = lane + 64 * e;
+      v[j][e] = (j < P.nsplit && d < a.head_dim) ? part[(int64_t)j * a.head_dim + d] : 0.f;
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float w =
-          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wi), s0 + j < 64 ? s0 + j : 63));
+  for (int j = 0; j < kMaxSplits; ++j) {
+    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wi), j));
 #pragma unroll
-      for (int e = 0; e < ND; ++e) acc[e] = fmaf(w, v[j][e], acc[e]);
-    }
+    for (int e = 0; e < ND; ++e) acc[e] = fmaf(w, v[j][e], acc[e]);
   }
   T* out = reinterpret_cast<T*>(a.out) + qrow * a.o_row + (int64_t)head * a.o_head;
 #pragma unroll
