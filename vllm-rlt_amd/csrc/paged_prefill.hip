@@ -396,11 +396,13 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, st[e]);
     } else {
+      // Key k0 + 4half + o (o = 8(e / 4) + e % 4) is visible when it is at
+      // most lim = min(qpos, end - 1) (-1 for a padding query): one compare
+      // against a per-lane bound per score.
+      const int bound = (q_ok ? min(qpos, end - 1) : -1) - k0 - 4 * half;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int kpos = k0 + 8 * (e >> 2) + 4 * half + (e & 3);
-        const bool vis = q_ok && kpos < end && kpos <= qpos;
-        st[e] = vis ? st[e] : -INFINITY;
+        st[e] = 8 * (e >> 2) + (e & 3) <= bound ? st[e] : -INFINITY;
         mx = fmaxf(mx, st[e]);
       }
     }
