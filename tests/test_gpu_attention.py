@@ -78,6 +78,20 @@ def test_decode_shapes(gpu, dtype, head_dim, heads, kv_heads):
     assert_close(actual, oracle_decode(q, k, v, tables, context), dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("head_dim", [320, 512])
+def test_decode_wide_heads_split_and_merge(gpu, dtype, head_dim):
+    """Head dims above 256 (up to the 512 the entry point accepts): rows long
+    enough for several splits, so the merge runs with 8 dims per lane."""
+    from vllm_rlt.kernels.hip_attention import paged_attention
+
+    lengths = [1, 64, 65, 300, 2000]
+    q, k, v, tables, context = random_paged(lengths, 4, 2, head_dim, dtype, gpu, block=16,
+                                            seed=head_dim)
+    actual = paged_attention(q, k, v, tables, context)
+    assert_close(actual, oracle_decode(q, k, v, tables, context), dtype)
+
+
 @pytest.mark.parametrize("block", [2, 3, 5, 16, 32])
 def test_decode_odd_block_sizes(gpu, block):
     from vllm_rlt.kernels.hip_attention import paged_attention
