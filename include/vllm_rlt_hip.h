@@ -121,9 +121,9 @@ int vrh_paged_decode(int dtype, void* out, const void* q, const void* key_cache,
  * Packed causal prefill, bottom-right aligned: sequence s owns query rows
  * [cu_seqlens_q[s], cu_seqlens_q[s+1]) and keys [0, context_lengths[s]) through
  * block_tables[s]; its query i sits at position n_s - q_s + i and attends keys
- * at positions <= that. bf16/f16 with head_dim a multiple of 32 (<= 224) use
- * MFMA tiles with fp32 accumulation; other cases compute each query row with
- * the decode kernel. With a workspace of
+ * at positions <= that. bf16/f16 with head_dim 32, 64, 96 or 128 (and
+ * 16-byte aligned rows) use MFMA tiles with fp32 accumulation; other cases
+ * compute each query row with the decode kernel. With a workspace of
  * vrh_paged_prefill_workspace_bytes(num_seqs, q_heads, head_dim) bytes,
  * sequences of one query (decode rows riding in a packed batch) use split-KV
  * decode, and the MFMA work items are dispatched longest sequence first (a

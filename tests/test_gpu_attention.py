@@ -260,6 +260,50 @@ def test_packed_prefill_block_sizes_and_long_tables(gpu, block, dtype, head_dim,
     assert_close(actual, oracle_prefill(q, k, v, tables, lengths, cu), dtype)
 
 
+@pytest.mark.parametrize("dtype,head_dim,heads,kv_heads", [(torch.bfloat16, 128, 8, 8),
+                                                          (torch.float16, 64, 8, 2)])
+def test_packed_prefill_long_sequences_ragged_queries(gpu, dtype, head_dim, heads, kv_heads):
+    """Long prefixes (up to 5000 keys) with ragged query counts and decode rows
+    in one packed batch, bf16 MHA and f16 GQA; also replayed from a captured
+    graph."""
+    from vllm_rlt.kernels.hip_attention import paged_prefill_attention
+
+    sequences = [(4000, 300), (3000, 512), (2500, 1), (5000, 129), (1500, 64), (1100, 2),
+                 (300, 40)]
+    gen = torch.Generator().manual_seed(23)
+    block = 16
+    pages = sum(-(-n // block) for n, _ in sequences)
+    k = torch.randn(pages, block, kv_heads, head_dim, generator=gen).to(dtype).to(gpu)
+    v = torch.randn(pages, block, kv_heads, head_dim, generator=gen).to(dtype).to(gpu)
+    order = torch.randperm(pages, generator=gen).tolist()
+    width = max(-(-n // block) for n, _ in sequences)
+    tables = torch.full((len(sequences), width), -1, dtype=torch.int32)
+    for s, (n, _) in enumerate(sequences):
+        ids = [order.pop() for _ in range(-(-n // block))]
+        tables[s, : len(ids)] = torch.tensor(ids, dtype=torch.int32)
+    total = sum(c for _, c in sequences)
+    q = torch.randn(total, heads, head_dim, generator=gen).to(dtype).to(gpu)
+    cu = torch.tensor(np.cumsum([0] + [c for _, c in sequences]), dtype=torch.int32, device=gpu)
+    lengths = torch.tensor([n for n, _ in sequences], dtype=torch.int32, device=gpu)
+    tables = tables.to(gpu)
+    expected = oracle_prefill(q, k, v, tables, lengths, cu)
+    actual = paged_prefill_attention(q, k, v, tables, lengths, cu, 512)
+    assert_close(actual, expected, dtype)
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        paged_prefill_attention(q, k, v, tables, lengths, cu, 512)
+    torch.cuda.current_stream().wait_stream(stream)
+    with torch.cuda.graph(graph):
+        captured = paged_prefill_attention(q, k, v, tables, lengths, cu, 512)
+    for _ in range(3):
+        captured.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, actual)
+
+
 def test_packed_prefill_mixed_with_decode_rows(gpu):
     """WCPB shape in miniature: long chunks with prefixes and q_len = 1 rows."""
     from vllm_rlt.kernels.hip_attention import paged_prefill_attention
