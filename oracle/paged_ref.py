@@ -225,7 +225,12 @@ def blocks_to_host(key_pool, value_pool, blocks):
 
 
 def blocks_from_host(key_pool, value_pool, blocks, host_keys, host_values):
-    """core/kv_cache_manager.py:504-523: ``key_cache[block] = snapshot.keys[row]``."""
+    """core/kv_cache_manager.py:504-523: ``key_cache[block] = snapshot.keys[row]``.
+    A snapshot restores only into as many pages as it holds (the page-count
+    refusal of :513-516); anything else raises ``ValueError``."""
+    blocks = np.asarray(blocks, dtype=np.int64)
+    if len(blocks) != len(host_keys) or len(blocks) != len(host_values):
+        raise ValueError("snapshot page count differs from the restore target")
     for row, block in enumerate(np.asarray(blocks, dtype=np.int64)):
         key_pool[block] = host_keys[row]
         value_pool[block] = host_values[row]

@@ -381,3 +381,20 @@ def test_prefill_without_workspace_runs_decode_rows_through_mfma_tiles(gpu):
     expected = oracle_prefill(q, k, v, tables, lengths, cu)
     assert_close(out, expected, torch.bfloat16)
     assert_close(routed, expected, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype,head_dim", [(torch.float32, 128), (torch.bfloat16, 48)])
+def test_packed_prefill_fallback_ignores_padding_rows(gpu, dtype, head_dim):
+    """A bucketed q longer than cu_seqlens_q[-1] on the per-row fallback (f32,
+    and a head dim without MFMA tiles): the padding rows belong to no sequence
+    and are skipped (they must not read past a table's padded entries); the
+    valid rows match the oracle."""
+    from vllm_rlt.kernels.hip_attention import paged_prefill_attention
+
+    sequences = [(70, 5), (33, 25)]
+    q, k, v, tables, lengths, cu, max_q = prefill_inputs(sequences, 4, 2, head_dim, dtype, gpu)
+    tables[1, 3:] = -1  # pad past the 3 pages of 33 keys, as the metadata planner does
+    padded = torch.cat([q, torch.randn(9, *q.shape[1:], device=gpu).to(dtype)])
+    actual = paged_prefill_attention(padded, k, v, tables, lengths, cu, max_q)
+    torch.cuda.synchronize()
+    assert_close(actual[: q.shape[0]], oracle_prefill(q, k, v, tables, lengths, cu), dtype)

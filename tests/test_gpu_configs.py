@@ -1,0 +1,251 @@
+"""GPU parity at the benchmark configurations' own shapes (the seeded
+generators of vllm_rlt.workloads), as the reference's GPU tests run its path
+at served shapes (tests/test_attention.py:281-379).
+
+Appends, finalize and block copies are bit-exact; attention is checked against
+the CPU oracle (oracle/paged_ref.py) within max-abs 2e-2 and rtol 1e-2 for
+bf16 (1e-4 for fp32). The oracle runs per row over that row's own pages,
+gathered from the device pool and relabelled 0..pages-1 (the same keys in the
+same order, so the same result); where a configuration has thousands of query
+rows it runs on a seeded subsample that is named in the test.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+BS = 16
+
+
+def np32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def oracle_rows(q, kc, vc, tables, lengths, q_rows, table_rows=None, dtype="bf16"):
+    """Oracle outputs of query rows ``q_rows``; row j reads table row
+    ``table_rows[j]`` (default: the same index) with length ``lengths[j]``."""
+    table_rows = q_rows if table_rows is None else table_rows
+    out = []
+    for qr, tr, n in zip(q_rows, table_rows, lengths):
+        n = int(n)
+        pages = -(-n // BS)
+        if n == 0:
+            out.append(np.zeros((1, *q.shape[1:]), np.float32))
+            continue
+        idx = tables[tr, :pages].long()
+        keys, values = np32(kc[idx]), np32(vc[idx])
+        o = ref.paged_attention(np32(q[qr : qr + 1]), keys, values,
+                                np.arange(pages, dtype=np.int64)[None], np.array([n]))
+        out.append(o)
+    return ref.round_to(np.concatenate(out), dtype)
+
+
+def assert_attention(actual, expected, atol=2e-2, rtol=1e-2):
+    np.testing.assert_allclose(np32(actual), expected, atol=atol, rtol=rtol)
+
+
+@pytest.fixture
+def free_gpu_memory():
+    yield
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def test_config1_full_fp32(gpu, free_gpu_memory):
+    """Config 1 in full: 8 fp32 rows, append at n, attend with n + 1."""
+    from vllm_rlt.kernels.hip_attention import kv_append, paged_attention
+    from vllm_rlt.workloads import config1
+
+    print("config1: 8 rows fp32, full", flush=True)
+    w = config1(device=gpu)
+    kc, vc = w.key_cache[:, 0], w.value_cache[:, 0]
+    expected_k, expected_v = np32(kc), np32(vc)
+    ref.kv_append(expected_k, expected_v, np32(w.k_new[0]), np32(w.v_new[0]),
+                  w.write_blocks.cpu().numpy(), w.write_offsets.cpu().numpy())
+    kv_append(kc, vc, w.k_new[0], w.v_new[0], w.write_blocks, w.write_offsets)
+    out = paged_attention(w.q, kc, vc, w.block_tables, w.context_lengths)
+    torch.cuda.synchronize()
+    assert np.array_equal(np32(kc), expected_k) and np.array_equal(np32(vc), expected_v)
+    want = ref.paged_attention(np32(w.q), expected_k, expected_v, w.block_tables.cpu().numpy(),
+                               w.context_lengths.cpu().numpy())
+    assert_attention(out, want, atol=1e-4, rtol=1e-4)
+
+
+def test_config2_append_decode_finalize(gpu, free_gpu_memory):
+    """Config 2: all 64 rows on one layer view of the 24-layer, 4-plane pool;
+    the 24-layer batched append; LAST_EXITED finalize of every row's token."""
+    from vllm_rlt.kernels.hip_attention import (
+        kv_append, kv_append_layers, kv_finalize, paged_attention)
+    from vllm_rlt.workloads import config2
+
+    print("config2: 64 rows, 24-layer pool of 4 depth planes", flush=True)
+    w = config2(device=gpu)
+    layer = 7
+    wb, wo = w.write_blocks, w.write_offsets
+    before_other = w.key_cache[wb, layer + 1, wo].clone()
+    kc, vc = w.key_cache[:, layer], w.value_cache[:, layer]
+    kv_append(kc, vc, w.k_new[layer], w.v_new[layer], wb, wo)
+    torch.cuda.synchronize()
+    assert torch.equal(kc[wb, wo], w.k_new[layer]) and torch.equal(vc[wb, wo], w.v_new[layer])
+    assert torch.equal(w.key_cache[wb, layer + 1, wo], before_other)
+
+    out = paged_attention(w.q, kc, vc, w.block_tables, w.context_lengths)
+    torch.cuda.synchronize()
+    rows = list(range(w.rows))
+    want = oracle_rows(w.q, kc, vc, w.block_tables, w.context_lengths.cpu(), rows)
+    assert_attention(out, want)
+
+    # every layer of the step in one launch
+    kv_append_layers(w.key_cache, w.value_cache, 0, w.k_new, w.v_new, wb, wo)
+    torch.cuda.synchronize()
+    assert torch.equal(w.key_cache[wb, :, wo].transpose(0, 1), w.k_new)
+    assert torch.equal(w.value_cache[wb, :, wo].transpose(0, 1), w.v_new)
+
+    # finalize: each row's token exits at its depth; deeper planes get its KV
+    depths = w.extra["depths"]
+    planes = 4
+    plane_tables = w.extra["plane_tables"]
+    width = w.block_tables.shape[1]
+    tables = torch.full((w.rows * planes, width), -1, dtype=torch.int32)
+    for i, pages in enumerate(plane_tables):
+        tables[i, : len(pages)] = torch.tensor(pages, dtype=torch.int32)
+    pos = (w.context_lengths.cpu() - 1).to(torch.int64)
+    descriptors = torch.stack([torch.arange(w.rows), depths.to(torch.int64), pos], dim=1)
+    page, off = pos // BS, pos % BS
+    blocks = tables.view(w.rows, planes, width)[torch.arange(w.rows)[:, None],
+                                                 torch.arange(planes)[None], page[:, None]]
+    blocks = blocks.to(torch.int64).to(gpu)  # [rows, planes]
+    before = w.key_cache[blocks, :, off.to(gpu)[:, None]].clone()  # [rows, planes, L, H, D]
+    kv_finalize(w.key_cache, w.value_cache, descriptors.to(gpu), tables.to(gpu), planes)
+    torch.cuda.synchronize()
+    after_k = w.key_cache[blocks, :, off.to(gpu)[:, None]]
+    after_v = w.value_cache[blocks, :, off.to(gpu)[:, None]]
+    for r in range(w.rows):
+        d = int(depths[r])
+        for p in range(planes):
+            if p <= d:
+                assert torch.equal(after_k[r, p], before[r, p]), (r, p)
+            else:
+                assert torch.equal(after_k[r, p], after_k[r, d]), (r, p)
+                assert torch.equal(after_v[r, p], after_v[r, d]), (r, p)
+    assert torch.equal(after_k[torch.arange(w.rows), depths.to(gpu)].transpose(0, 1), w.k_new)
+
+
+def test_config3_shared_prefix_cow_and_decode(gpu, free_gpu_memory):
+    """Config 3: 128 rows in 16 groups aliasing refcounted prefix pages,
+    mid-page appends, a copy-on-write copy of one shared page followed by a
+    divergent write, then decode of every row against the oracle."""
+    from vllm_rlt.kernels.hip_attention import kv_append, kv_copy_blocks, paged_attention
+    from vllm_rlt.workloads import config3
+
+    print("config3: 128 rows, shared prefixes, CoW", flush=True)
+    w = config3(device=gpu, spare_blocks=4)
+    kc, vc = w.key_cache[:, 0], w.value_cache[:, 0]
+    assert bool((w.write_offsets != 0).any()), "appends must land mid-page"
+    kv_append(kc, vc, w.k_new[0], w.v_new[0], w.write_blocks, w.write_offsets)
+    torch.cuda.synchronize()
+    assert torch.equal(kc[w.write_blocks, w.write_offsets], w.k_new[0])
+
+    # row 0 diverges inside its group's last shared prefix page
+    tables = w.block_tables.clone()
+    shared = int(tables[0, 63])
+    spare = int(w.extra["spare_blocks"][0])
+    assert all(int(tables[r, 63]) == shared for r in range(8))
+    kv_copy_blocks(w.key_cache, w.value_cache,
+                   torch.tensor([shared], dtype=torch.int64, device=gpu),
+                   torch.tensor([spare], dtype=torch.int64, device=gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(w.key_cache[spare], w.key_cache[shared])
+    assert torch.equal(w.value_cache[spare], w.value_cache[shared])
+    tables[0, 63] = spare
+    gen = torch.Generator().manual_seed(9)
+    k_div = torch.randn(1, 16, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    v_div = torch.randn(1, 16, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    shared_slot = kc[shared, 5].clone()
+    kv_append(kc, vc, k_div, v_div, torch.tensor([spare], dtype=torch.int64, device=gpu),
+              torch.tensor([5], dtype=torch.int64, device=gpu))
+    out = paged_attention(w.q, kc, vc, tables, w.context_lengths)
+    torch.cuda.synchronize()
+    assert torch.equal(kc[spare, 5], k_div[0]) and torch.equal(vc[spare, 5], v_div[0])
+    assert torch.equal(kc[shared, 5], shared_slot)
+    rows = list(range(w.rows))
+    want = oracle_rows(w.q, kc, vc, tables, w.context_lengths.cpu(), rows)
+    assert_attention(out, want)
+    # row 0 no longer reads the shared page, whose token differs
+    assert not torch.equal(out[0], paged_attention(w.q[:1], kc, vc, w.block_tables[:1],
+                                                   w.context_lengths[:1])[0])
+
+
+def test_config4_chunks_and_decode_rows(gpu, free_gpu_memory):
+    """Config 4: all 16 prefill chunks and 48 decode rows appended (bit-exact)
+    and attended in one packed call. Oracle on a seeded subsample: each chunk's
+    first and last query plus 6 random ones, and every decode row."""
+    from vllm_rlt.kernels.hip_attention import kv_append, paged_prefill_attention
+    from vllm_rlt.workloads import config4
+
+    print("config4: 16 chunks + 48 decode rows", flush=True)
+    w = config4(device=gpu)
+    kc, vc = w.key_cache[:, 0], w.value_cache[:, 0]
+    kv_append(kc, vc, w.k_new, w.v_new, w.write_blocks, w.write_offsets)
+    torch.cuda.synchronize()
+    assert torch.equal(kc[w.write_blocks, w.write_offsets], w.k_new)
+    assert torch.equal(vc[w.write_blocks, w.write_offsets], w.v_new)
+    out = paged_prefill_attention(w.q, kc, vc, w.block_tables, w.context_lengths,
+                                  w.cu_seqlens_q, w.max_seqlen_q)
+    torch.cuda.synchronize()
+    cu = w.cu_seqlens_q.tolist()
+    n = w.context_lengths.tolist()
+    gen = torch.Generator().manual_seed(11)
+    q_rows, t_rows, lengths = [], [], []
+    for s in range(len(n)):
+        q_len = cu[s + 1] - cu[s]
+        if q_len > 1:
+            picks = {0, q_len - 1, *torch.randint(0, q_len, (6,), generator=gen).tolist()}
+        else:
+            picks = {0}
+        for i in sorted(picks):
+            q_rows.append(cu[s] + i)
+            t_rows.append(s)
+            lengths.append(n[s] - q_len + i + 1)
+    want = oracle_rows(w.q, kc, vc, w.block_tables, lengths, q_rows, t_rows)
+    assert_attention(out[q_rows], want)
+
+
+def test_config5_long_context_decode(gpu, free_gpu_memory):
+    """Config 5's decode shape: 256 rows with context U[2048, 32768] over a
+    48-layer pool stride and 2048-page tables (a 4096-block pool here; the bench
+    uses the full ~200 GB one). Oracle on a seeded 12-row subsample that
+    includes the longest and the shortest row."""
+    from vllm_rlt.kernels.hip_attention import kv_append, paged_attention
+    from vllm_rlt.workloads import config5
+
+    print("config5: 256 rows, ctx up to 32768, 48-layer stride", flush=True)
+    w = config5(device=gpu, pool_blocks=4096)
+    layer = 31
+    kc, vc = w.key_cache[:, layer], w.value_cache[:, layer]
+    kv_append(kc, vc, w.k_new[0], w.v_new[0], w.write_blocks, w.write_offsets)
+    out = paged_attention(w.q, kc, vc, w.block_tables, w.context_lengths)
+    torch.cuda.synchronize()
+    # rows draw pages at random, so two rows may write one slot (which row
+    # lands is unspecified); every slot written by one row only is exact
+    addresses = (w.write_blocks * BS + w.write_offsets).tolist()
+    writers = {}
+    for r, a in enumerate(addresses):
+        writers.setdefault(a, []).append(r)
+    single = [(a, rs[0]) for a, rs in writers.items() if len(rs) == 1]
+    assert len(single) > 200
+    idx = torch.tensor([a for a, _ in single], device=gpu)
+    src = torch.tensor([r for _, r in single], device=gpu)
+    assert torch.equal(kc[idx // BS, idx % BS], w.k_new[0, src])
+    assert torch.equal(vc[idx // BS, idx % BS], w.v_new[0, src])
+    lengths = w.context_lengths.cpu()
+    gen = torch.Generator().manual_seed(12)
+    rows = {int(lengths.argmax()), int(lengths.argmin()),
+            *torch.randint(0, w.rows, (10,), generator=gen).tolist()}
+    rows = sorted(rows)
+    want = oracle_rows(w.q, kc, vc, w.block_tables, lengths[rows], rows)
+    assert_attention(out[rows], want)

@@ -9,7 +9,10 @@ head mapping, off-by-one window or causal length, dropped rows):
     window == slicing the history, the closed-form early-exit means of
     tests/test_kv_cache.py:61-77;
   * the committed golden fixture (tests/golden/decode_small.npz);
-  * integer kernels against brute-force loops / literal vectors.
+  * integer kernels against brute-force loops / literal vectors, including the
+    packed-address vectors of tests/test_flash_attention.py:121-143;
+  * finalize_token and the snapshot copies against the closed forms of
+    tests/test_kv_cache.py:38-58 and :261-303.
 """
 
 import math
@@ -288,3 +291,80 @@ def test_torch_cpu_restatement_matches_numpy_oracle():
     got = torch_ref.paged_attention(q, kc, vc, tables, lengths)
     want = ref.paged_attention(q.numpy(), kc.numpy(), vc.numpy(), tables.numpy(), lengths.numpy())
     np.testing.assert_allclose(got.numpy(), want, rtol=1e-5, atol=1e-6)
+
+
+def test_expand_kv_addresses_literal_packed_vectors():
+    """tests/test_flash_attention.py:121-143: two packed sequences with
+    positions [7, 8, 9] and [3, 4] on 4-token pages (context lengths [10, 5],
+    cu_seqlens_q [0, 3, 5]); blocks and offsets written out by hand for the
+    tables [10, 11, 12] and [20, 21]."""
+    tables = np.array([[10, 11, 12], [20, 21, -1]], np.int32)
+    blocks, offsets = ref.expand_kv_addresses([7, 8, 9, 3, 4], [0, 0, 0, 1, 1], tables, 4)
+    assert blocks.tolist() == [11, 12, 12, 20, 21]
+    assert offsets.tolist() == [3, 0, 1, 3, 0]
+    rows, lengths = ref.prefill_rows(tables, np.array([10, 5]), np.array([0, 3, 5]))
+    assert lengths.tolist() == [8, 9, 10, 4, 5]  # position + 1 of each packed query
+    # a page size of 1 makes every position its own page
+    blocks, offsets = ref.expand_kv_addresses([2, 0], [1, 0], tables, 1)
+    assert blocks.tolist() == [-1, 10] and offsets.tolist() == [0, 0]
+
+
+def test_finalize_token_closed_form():
+    """tests/test_kv_cache.py:38-58: token 0 of a 3-plane request is written at
+    depths 0 and 1 of both layers with keys 10 * layer + depth (values + 100)
+    and exits at depth 1. Plane 2 then holds depth 1's keys and values in
+    every layer, plane 0 keeps its own, and nothing else changes."""
+    blocks, layers, bs = 6, 2, 2
+    key_pool = np.full((blocks, layers, bs, 1, 4), -7.0, np.float32)
+    value_pool = key_pool.copy()
+    plane_block = {0: 4, 1: 1, 2: 3}  # page 0 of each plane
+    for layer in range(layers):
+        for depth in (0, 1):
+            key_pool[plane_block[depth], layer, 0] = 10 * layer + depth
+            value_pool[plane_block[depth], layer, 0] = 10 * layer + depth + 100
+    k0, v0 = key_pool.copy(), value_pool.copy()
+    ref.finalize_token(key_pool, value_pool, plane_block[1], [plane_block[2]], 0, [0, 1])
+    for layer in range(layers):
+        np.testing.assert_array_equal(key_pool[3, layer, 0], np.full((1, 4), 10 * layer + 1.0))
+        np.testing.assert_array_equal(value_pool[3, layer, 0], np.full((1, 4), 10 * layer + 101.0))
+        np.testing.assert_array_equal(key_pool[4, layer, 0], np.full((1, 4), 10.0 * layer))
+    changed = key_pool != k0
+    assert changed.sum() == changed[3, :, 0].size and changed[3, :, 0].all()
+    assert ((value_pool != v0).sum()) == changed.sum()
+    # physical copies: a later write at depth 1 does not reach plane 2
+    key_pool[1, 0, 0] = 0.0
+    np.testing.assert_array_equal(key_pool[3, 0, 0], np.ones((1, 4)))
+    # an empty layer list or destination list changes nothing
+    k1 = key_pool.copy()
+    ref.finalize_token(key_pool, value_pool, 1, [], 0, [0, 1])
+    ref.finalize_token(key_pool, value_pool, 1, [5], 0, [])
+    np.testing.assert_array_equal(key_pool, k1)
+
+
+def test_snapshot_round_trip_and_page_count_refusal():
+    """tests/test_kv_cache.py:261-303: pages go to host rows in table order and
+    come back into other blocks of a disturbed pool, byte for byte; a
+    snapshot is refused by a restore target with another page count."""
+    shape = (8, 2, 2, 1, 3)
+    slot = int(np.prod(shape[1:]))
+    key_pool = np.arange(np.prod(shape), dtype=np.float32).reshape(shape)
+    value_pool = -key_pool - 1
+    keys, values = ref.blocks_to_host(key_pool, value_pool, [5, 2, 7])
+    for row, block in enumerate([5, 2, 7]):
+        np.testing.assert_array_equal(keys[row].ravel(), block * slot + np.arange(slot))
+        np.testing.assert_array_equal(values[row].ravel(), -(block * slot + np.arange(slot)) - 1)
+    keys_before = keys.copy()
+    key_pool[5] = 0.0  # the host rows are copies, not views
+    np.testing.assert_array_equal(keys, keys_before)
+    target_k = np.full(shape, 9.0, np.float32)
+    target_v = target_k.copy()
+    ref.blocks_from_host(target_k, target_v, [1, 0, 3], keys, values)
+    for row, block in enumerate([1, 0, 3]):
+        np.testing.assert_array_equal(target_k[block], keys_before[row])
+        np.testing.assert_array_equal(target_v[block], values[row])
+    untouched = [b for b in range(8) if b not in (1, 0, 3)]
+    assert (target_k[untouched] == 9.0).all() and (target_v[untouched] == 9.0).all()
+    with pytest.raises(ValueError, match="page count"):
+        ref.blocks_from_host(target_k, target_v, [1, 0], keys, values)
+    with pytest.raises(ValueError, match="page count"):
+        ref.blocks_from_host(target_k, target_v, [1, 0, 3, 4], keys, values)

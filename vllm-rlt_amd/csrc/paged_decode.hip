@@ -131,6 +131,9 @@ __device__ __forceinline__ int row_length(int64_t row, const DecodeArgs& a, int6
     seq = (int)(row / a.expand_e);
     i = (int)(row - (int64_t)seq * a.expand_e);
   } else {
+    // Rows outside [cu_q[0], cu_q[num_seqs]) (padding of a bucketed q) belong
+    // to no sequence.
+    if (row < a.cu_q[0] || row >= a.cu_q[a.num_seqs]) return -1;
     int lo = 0, hi = a.num_seqs - 1;  // last s with cu_q[s] <= row
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -140,7 +143,7 @@ __device__ __forceinline__ int row_length(int64_t row, const DecodeArgs& a, int6
     i = (int)(row - a.cu_q[lo]);
   }
   const int q_len = a.cu_q[seq + 1] - a.cu_q[seq];
-  if (a.expand_e > 0 && (q_len > a.expand_e || i >= q_len)) return -1;
+  if (i < 0 || i >= q_len || (a.expand_e > 0 && q_len > a.expand_e)) return -1;
   *table_row = seq;
   *query_row = a.cu_q[seq] + i;
   return clamp_length(a.lengths[seq] - q_len + i + 1, a);

@@ -16,6 +16,13 @@ Configurations (shape symbols: Hq = Hkv = 16, D = 128, block_size 16):
   4  WCPB prefill + decode: 16 prompts ~ U[1024, 8192] in 512-token chunks, one
      chunk per prompt at a random chunk index and depth ~ U{0..3}, prefix =
      index * 512 at that depth; plus 48 decode rows with context ~ U[256, 4096].
+  5  Ouro-2.6B decode shape: 256 rows, context ~ U[2048, 32768], a 48-layer
+     pool (6 MiB of K+V per block in bf16) of ``pool_blocks`` blocks and
+     2048-page tables. The resident context (~4.4M tokens x 48 layers) exceeds
+     any one GPU, so rows draw their pages from the pool at random: each row's
+     pages are distinct, rows may share pages (the per-row bytes are counted
+     as read, as for shared prefixes). Appends land at position n - 1 of each
+     row (its last page).
 """
 
 from __future__ import annotations
@@ -165,8 +172,10 @@ def config2(device="cpu", rows=64, layers=24, depths=4, ctx_low=512, ctx_high=40
 
 
 def config3(device="cpu", groups=16, per_group=8, prefix_pages=64, suffix_low=64,
-            suffix_high=1024, layers=1, dtype=torch.bfloat16, fill=True) -> DecodeWorkload:
-    """SHARED layout: each group's requests alias the same prefix pages."""
+            suffix_high=1024, layers=1, dtype=torch.bfloat16, fill=True,
+            spare_blocks=0) -> DecodeWorkload:
+    """SHARED layout: each group's requests alias the same prefix pages.
+    ``spare_blocks`` free blocks follow the assigned ones (copy-on-write targets)."""
     g_tab, g_val, g_len = _gens()
     rows = groups * per_group
     suffix = _randint(g_len, suffix_low, suffix_high, rows)
@@ -174,8 +183,9 @@ def config3(device="cpu", groups=16, per_group=8, prefix_pages=64, suffix_low=64
     lengths = ctx + 1
     private = [int((lengths[r] + BLOCK - 1) // BLOCK) - prefix_pages for r in range(rows)]
     counts = [prefix_pages] * groups + private
-    num_blocks = sum(counts)
-    assigned = _scatter_pages(g_tab, counts, num_blocks)
+    num_blocks = sum(counts) + spare_blocks
+    assigned = _scatter_pages(g_tab, counts + [spare_blocks], num_blocks)
+    spare = assigned.pop()
     tables = [assigned[r // per_group] + assigned[groups + r] for r in range(rows)]
     width = max(len(t) for t in tables)
     shape = (num_blocks, layers, BLOCK, HEADS, HEAD_DIM)
@@ -194,7 +204,38 @@ def config3(device="cpu", groups=16, per_group=8, prefix_pages=64, suffix_low=64
                           v_new, _table_tensor(tables, width).to(device),
                           lengths.to(torch.int32).to(device), wb.to(device), wo.to(device),
                           extra={"prefix_tables": assigned[:groups],
-                                 "unique_tokens": unique_tokens})
+                                 "unique_tokens": unique_tokens, "spare_blocks": spare})
+
+
+def config5(device="cpu", rows=256, ctx_low=2048, ctx_high=32768, layers=48,
+            pool_blocks=32768, width=2048, dtype=torch.bfloat16, fill=True) -> DecodeWorkload:
+    """Long-context decode over a 48-layer pool (see the module docstring)."""
+    g_tab, g_val, g_len = _gens()
+    lengths = _randint(g_len, ctx_low, ctx_high, rows)
+    pages = ((lengths + BLOCK - 1) // BLOCK).tolist()
+    if max(pages) > min(width, pool_blocks):
+        raise ValueError("contexts exceed the table width or the pool")
+    order = torch.randperm(pool_blocks, generator=g_tab)
+    starts = torch.randint(0, pool_blocks, (rows,), generator=g_tab)
+    tables = torch.full((rows, width), -1, dtype=torch.int32)
+    for r in range(rows):
+        idx = (int(starts[r]) + torch.arange(pages[r])) % pool_blocks
+        tables[r, : pages[r]] = order[idx].to(torch.int32)
+    shape = (pool_blocks, layers, BLOCK, HEADS, HEAD_DIM)
+    key_cache = torch.empty(shape, dtype=dtype, device=device)
+    value_cache = torch.empty_like(key_cache)
+    if fill:
+        _fill_pool(key_cache, g_val, 0.5)
+        _fill_pool(value_cache, g_val, 0.5)
+    q = _values(g_val, (rows, HEADS, HEAD_DIM), dtype, 0.5, device)
+    k_new = _values(g_val, (1, rows, HEADS, HEAD_DIM), dtype, 0.5, device)
+    v_new = _values(g_val, (1, rows, HEADS, HEAD_DIM), dtype, 0.5, device)
+    last = (lengths - 1).to(torch.int64)
+    wb = tables[torch.arange(rows), last // BLOCK].to(torch.int64)
+    wo = last % BLOCK
+    return DecodeWorkload("config5", dtype, layers, pool_blocks, key_cache, value_cache, q, k_new,
+                          v_new, tables.to(device), lengths.to(torch.int32).to(device),
+                          wb.to(device), wo.to(device))
 
 
 @dataclass
