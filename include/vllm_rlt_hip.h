@@ -28,6 +28,7 @@
  *                            kernels/graph_kv.py:7-65 (write_graph_kv)
  *   vrh_paged_decode         kernels/paged_attention.py:12-71 (torch_paged_attention
  *                            and its windowed variant), kernels/triton_attention.py:150-202
+ *   vrh_paged_decode_noalloc (none: see its declaration)
  *   vrh_paged_prefill        kernels/triton_attention.py:313-366 (paged_prefill_attention)
  *   vrh_kv_gather            kv_cache_manager.py:834-854 (read)
  *   vrh_kv_finalize          kernels/routing.py:147-177 (finalize_kernel),
@@ -116,6 +117,31 @@ int vrh_paged_decode(int dtype, void* out, const void* q, const void* key_cache,
                      int64_t k_token_stride, int64_t k_head_stride, int64_t v_block_stride,
                      int64_t v_token_stride, int64_t v_head_stride, int32_t window,
                      void* workspace, size_t workspace_bytes, vrh_stream_t stream);
+
+/* ------------------------------------------------- paged decode, no alloc
+ * No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP-graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same computation and kernels as vrh_paged_decode, with
+ * the split partials in a built-in device array of
+ * VRH_PAGED_DECODE_NOALLOC_MAX_BYTES per GPU (held until the process ends)
+ * instead of a workspace argument. Calls needing more than that
+ * (vrh_paged_decode_workspace_bytes(rows, q_heads, head_dim) > the limit, e.g.
+ * more than 378 rows x 16 heads at head_dim 128) fail with
+ * VRH_ERROR_INVALID_ARG before any launch. Every call on one GPU shares that
+ * array: calls that overlap on one GPU (other streams, concurrent graph
+ * replays) race. Nothing in it needs clearing between calls. */
+#define VRH_PAGED_DECODE_NOALLOC_MAX_BYTES ((size_t)96 << 20)
+size_t vrh_paged_decode_noalloc_max_bytes(void);
+int vrh_paged_decode_noalloc(int dtype, void* out, const void* q, const void* key_cache,
+                             const void* value_cache, const int32_t* block_tables,
+                             const int32_t* context_lengths, int64_t rows, int32_t q_heads,
+                             int32_t kv_heads, int32_t head_dim, int32_t block_size,
+                             int32_t table_width, int64_t table_stride, int64_t q_row_stride,
+                             int64_t q_head_stride, int64_t out_row_stride,
+                             int64_t out_head_stride, int64_t k_block_stride,
+                             int64_t k_token_stride, int64_t k_head_stride,
+                             int64_t v_block_stride, int64_t v_token_stride,
+                             int64_t v_head_stride, int32_t window, vrh_stream_t stream);
 
 /* ----------------------------------------------------------- paged prefill
  * Packed causal prefill, bottom-right aligned: sequence s owns query rows

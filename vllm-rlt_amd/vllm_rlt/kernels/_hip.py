@@ -19,7 +19,7 @@ from functools import cache
 LIBRARY_NAME = "libvllm_rlt_hip.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "_lib",
                             LIBRARY_NAME)
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 VRH_DTYPE_F32, VRH_DTYPE_F16, VRH_DTYPE_BF16 = 0, 1, 2
 
@@ -43,6 +43,12 @@ SIGNATURES: dict[str, tuple[object, list]] = {
         _INT,
         [_INT, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _SZ, _P],
+    ),
+    "vrh_paged_decode_noalloc_max_bytes": (_SZ, []),
+    "vrh_paged_decode_noalloc": (
+        _INT,
+        [_INT, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64,
+         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P],
     ),
     "vrh_paged_prefill": (
         _INT,

@@ -124,6 +124,40 @@ def paged_attention(q, key_cache, value_cache, block_tables, context_lengths, wi
     return output
 
 
+def paged_attention_noalloc(q, key_cache, value_cache, block_tables, context_lengths,
+                            window: int = 0, out=None):
+    """``paged_attention`` without a workspace allocation: the split partials use
+    the library's built-in per-GPU scratch (``vrh_paged_decode_noalloc``), and
+    ``out`` may be given so that the call allocates nothing at all. Calls that
+    overlap on one GPU share that scratch and race."""
+    if type(window) is not int or window < 0:
+        raise ValueError("window must be a nonnegative integer")
+    q, context_lengths = _attention_inputs(q, key_cache, value_cache, block_tables,
+                                           context_lengths)
+    rows = q.shape[0]
+    if block_tables.shape[0] != rows or context_lengths.shape[0] != rows:
+        raise ValueError("block_tables and context_lengths must have one row per query row")
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.device != q.device \
+            or out.stride(-1) != 1:
+        raise ValueError("out must match q's shape, dtype and device, with a contiguous head_dim")
+    if rows == 0:
+        return out
+    lib = library()
+    lib.check(
+        lib.vrh_paged_decode_noalloc(
+            dtype_code(q.dtype), out.data_ptr(), q.data_ptr(), key_cache.data_ptr(),
+            value_cache.data_ptr(), block_tables.data_ptr(), context_lengths.data_ptr(), rows,
+            q.shape[1], key_cache.shape[2], q.shape[2], key_cache.shape[1], block_tables.shape[1],
+            block_tables.stride(0), q.stride(0), q.stride(1), out.stride(0), out.stride(1),
+            *key_cache.stride()[:3], *value_cache.stride()[:3], window, _stream(q),
+        ),
+        "vrh_paged_decode_noalloc",
+    )
+    return out
+
+
 def paged_prefill_attention(q, key_cache, value_cache, block_tables, context_lengths,
                             cu_seqlens_q, max_seqlen_q):
     """Packed causal prefill, bottom-right aligned per sequence."""
