@@ -40,3 +40,26 @@ def paged_attention(q, key_cache, value_cache, block_tables, context_lengths):
         weights = torch.softmax(scores, dim=-1)
         out[row] = torch.einsum("hn,nhd->hd", weights, values.float()).to(q.dtype)
     return out
+
+
+def append(key_cache, value_cache, layer, k, v, write_blocks, write_offsets):
+    """The reference's eager append (core/kv_cache_manager.py:698-699): one
+    advanced-index put per cache, ``cache[blocks, layer, offsets] = k``, on a
+    whole pool ``[N, L, bs, H, D]``."""
+    key_cache[write_blocks, layer, write_offsets] = k
+    value_cache[write_blocks, layer, write_offsets] = v
+
+
+def prefill(q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q):
+    """Packed causal prefill as per-query decode rows (the expansion of the
+    reference's tests/test_attention.py:333-346): query i of sequence s reads
+    the sequence's table with length n_s - q_s + i + 1."""
+    tables, lengths = [], []
+    cu = cu_seqlens_q.tolist()
+    for s, n in enumerate(context_lengths.tolist()):
+        q_len = cu[s + 1] - cu[s]
+        for i in range(q_len):
+            tables.append(block_tables[s])
+            lengths.append(max(0, n - q_len + i + 1))
+    return paged_attention(q, key_cache, value_cache, torch.stack(tables),
+                           torch.tensor(lengths, dtype=torch.int32))

@@ -291,6 +291,24 @@ def test_torch_cpu_restatement_matches_numpy_oracle():
     got = torch_ref.paged_attention(q, kc, vc, tables, lengths)
     want = ref.paged_attention(q.numpy(), kc.numpy(), vc.numpy(), tables.numpy(), lengths.numpy())
     np.testing.assert_allclose(got.numpy(), want, rtol=1e-5, atol=1e-6)
+    # packed prefill as decode rows, against the numpy oracle's own expansion
+    cu = torch.tensor([0, 4, 5, 7], dtype=torch.int32)
+    qp = torch.randn(7, 4, 8, generator=gen)
+    got = torch_ref.prefill(qp, kc, vc, tables, lengths, cu)
+    want = ref.paged_prefill(qp.numpy(), kc.numpy(), vc.numpy(), tables.numpy(),
+                             lengths.numpy(), cu.numpy())
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-5, atol=1e-6)
+    # the index-put append is the oracle's append on the layer view (bit-exact)
+    pool_k = torch.randn(6, 3, 4, 2, 8, generator=gen)
+    pool_v = torch.randn(6, 3, 4, 2, 8, generator=gen)
+    k_new = torch.randn(5, 2, 8, generator=gen)
+    blocks = torch.tensor([4, 0, 4, 2, 5])
+    offsets = torch.tensor([1, 3, 2, 0, 3])
+    want_k, want_v = pool_k[:, 1].numpy().copy(), pool_v[:, 1].numpy().copy()
+    ref.kv_append(want_k, want_v, k_new.numpy(), -k_new.numpy(), blocks.numpy(), offsets.numpy())
+    torch_ref.append(pool_k, pool_v, 1, k_new, -k_new, blocks, offsets)
+    assert np.array_equal(pool_k[:, 1].numpy(), want_k)
+    assert np.array_equal(pool_v[:, 1].numpy(), want_v)
 
 
 def test_expand_kv_addresses_literal_packed_vectors():
