@@ -126,7 +126,7 @@ int vrh_paged_decode(int dtype, void* out, const void* q, const void* key_cache,
  * VRH_PAGED_DECODE_NOALLOC_MAX_BYTES per GPU (held until the process ends)
  * instead of a workspace argument. Calls needing more than that
  * (vrh_paged_decode_workspace_bytes(rows, q_heads, head_dim) > the limit, e.g.
- * more than 378 rows x 16 heads at head_dim 128) fail with
+ * more than 756 rows x 16 heads at head_dim 128) fail with
  * VRH_ERROR_INVALID_ARG before any launch. Every call on one GPU shares that
  * array: calls that overlap on one GPU (other streams, concurrent graph
  * replays) race. Nothing in it needs clearing between calls. */

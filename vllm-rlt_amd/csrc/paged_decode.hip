@@ -7,10 +7,10 @@
 //
 // Design (bandwidth-bound; every K/V byte is read exactly once per q head):
 //  * One 64-lane wavefront per (split, q head, row). A split is a run of whole
-//    pages: bps = max(min_bps, ceil(pages / kMaxSplits)) pages, so the
-//    partition depends only on the row's own length -> batch invariance.
-//    Short splits (64 tokens by default) keep ~36k waves in flight for the
-//    Ouro decode batch, which hides HBM latency and balances the tail.
+//    pages: bps = max(min_bps, ceil(pages / kMaxSplits)) pages (at least 128
+//    tokens, at most 16 splits per row), so the partition depends only on
+//    the row's own length -> batch invariance. The split index is rotated
+//    per (row, head) so that every XCD receives the same share of splits.
 //  * Lane layout: LPT lanes cover one token's head_dim with VEC elements each
 //    (16-byte global loads for bf16 D=128: LPT=16), so one wave-wide load
 //    instruction fetches TPL = 64 / LPT tokens; U loads of K and U of V are
@@ -39,7 +39,7 @@ namespace {
 #define VRH_DECODE_U 4
 #endif
 #ifndef VRH_SPLIT_TOKENS
-#define VRH_SPLIT_TOKENS 64
+#define VRH_SPLIT_TOKENS 128
 #endif
 #ifndef VRH_DECODE_NT
 #define VRH_DECODE_NT 1
@@ -48,7 +48,10 @@ namespace {
 #define VRH_DECODE_PREFETCH 1
 #endif
 
-constexpr int kMaxSplits = 32;
+#ifndef VRH_MAX_SPLITS
+#define VRH_MAX_SPLITS 16
+#endif
+constexpr int kMaxSplits = VRH_MAX_SPLITS;
 constexpr int kSplitTokens = VRH_SPLIT_TOKENS;  // minimum tokens per split (whole pages)
 constexpr int kU = VRH_DECODE_U;                // wave loads per chunk (K and V each)
 
@@ -149,17 +152,19 @@ __device__ __forceinline__ int row_length(int64_t row, const DecodeArgs& a, int6
   return clamp_length(a.lengths[seq] - q_len + i + 1, a);
 }
 
+// The work of one (row, q head) over splits split0, split0 + step, ... of
+// the row's partition: multi-split rows write (m, l, acc) partials, single
+// splits the output; a zero-length row writes zeros (from split 0).
 template <typename T, int VEC, int LPT>
-__global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
+__device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, int head,
+                                            int split0, int step) {
   constexpr int TPL = 64 / LPT;  // tokens per wave load
   constexpr int CH = kU * TPL;   // tokens per chunk
   using raw_t = typename Vec<T, VEC>::raw_t;
 
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   const int dg = lane % LPT;
   const int tg = lane / LPT;
-  const int head = blockIdx.y;
-  const int64_t row = a.row_base + blockIdx.z;
   const int kvh = head / a.group;
   int64_t trow, qrow;
   const int n = row_length(row, a, &trow, &qrow);
@@ -168,7 +173,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   T* out = reinterpret_cast<T*>(a.out) + qrow * a.o_row + (int64_t)head * a.o_head + dg * VEC;
 
   if (n == 0) {
-    if (blockIdx.x == 0 && tg == 0 && dvalid) {
+    if (split0 == 0 && tg == 0 && dvalid) {
       float z[VEC];
 #pragma unroll
       for (int i = 0; i < VEC; ++i) z[i] = 0.f;
@@ -177,8 +182,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
     return;
   }
   const Partition P = partition(n, a);
-  if ((int)blockIdx.x >= P.nsplit) return;
-
+  if (split0 >= P.nsplit) return;
   float qf[VEC];
   {
     const T* qp = reinterpret_cast<const T*>(a.q) + qrow * a.q_row + (int64_t)head * a.q_head +
@@ -199,7 +203,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)kvh * a.v_head + lane_dim;
   const int32_t* table = a.tables + trow * a.table_stride;
 
-  for (int split = blockIdx.x; split < P.nsplit; split += gridDim.x) {
+  for (int split = split0; split < P.nsplit; split += step) {
     const int b0 = P.first + split * P.bps;
     const int b1 = min(b0 + P.bps, P.first + P.pages);
     const int tb = max(P.start, b0 * a.block_size);
@@ -311,9 +315,63 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   }
 }
 
+// Grid form: one wave per (split column, q head, row).
+template <typename T, int VEC, int LPT>
+__global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
+  const int head = blockIdx.y;
+  const int64_t row = a.row_base + blockIdx.z;
+  // Workgroup L = x + gx * (head + heads * row) runs on XCD L % 8. Rows need
+  // different split counts, so with split = x the low split indices (present
+  // in every row) would pile onto the same XCDs; rotating the split index by
+  // (head + heads * row) spreads every split position evenly over the XCDs.
+  int split0 = (int)blockIdx.x - (int)((blockIdx.y + (int64_t)gridDim.y * blockIdx.z) % gridDim.x);
+  if (split0 < 0) split0 += gridDim.x;
+  decode_work<T, VEC, LPT>(a, row, head, split0, gridDim.x);
+}
+
+// Log-sum-exp merge of one (row, q head)'s split partials by one wave, for
+// head dims [d0, d0 + 64 * ND): lane s holds split s's weight; each lane owns
+// ND dims and issues the loads of all splits at once, then combines them in
+// split order.
+template <typename T, int ND>
+__device__ __forceinline__ void merge_partials(const DecodeArgs& a, int64_t row, int head,
+                                               int64_t qrow, int nsplit, int lane, int d0) {
+  const int64_t idx0 = (row * a.q_heads + head) * kMaxSplits;
+  const bool live = lane < nsplit;
+  const float mi = live ? a.part_ml[(idx0 + lane) * 2 + 0] : -INFINITY;
+  const float li = live ? a.part_ml[(idx0 + lane) * 2 + 1] : 0.f;
+  const float M = wave_max(mi);
+  const float wi = live ? fast_exp2(mi - M) : 0.f;
+  const float L = wave_sum(wi * li);
+  const float inv = fast_rcp(fmaxf(L, 1e-30f));
+  const float* part = a.part_acc + idx0 * a.head_dim;
+  float acc[ND];
+#pragma unroll
+  for (int e = 0; e < ND; ++e) acc[e] = 0.f;
+  float v[kMaxSplits][ND];
+#pragma unroll
+  for (int j = 0; j < kMaxSplits; ++j)
+#pragma unroll
+    for (int e = 0; e < ND; ++e) {
+      const int d = d0 + lane + 64 * e;
+      v[j][e] = (j < nsplit && d < a.head_dim) ? part[(int64_t)j * a.head_dim + d] : 0.f;
+    }
+#pragma unroll
+  for (int j = 0; j < kMaxSplits; ++j) {
+    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wi), j));
+#pragma unroll
+    for (int e = 0; e < ND; ++e) acc[e] = fmaf(w, v[j][e], acc[e]);
+  }
+  T* out = reinterpret_cast<T*>(a.out) + qrow * a.o_row + (int64_t)head * a.o_head;
+#pragma unroll
+  for (int e = 0; e < ND; ++e) {
+    const int d = d0 + lane + 64 * e;
+    if (d < a.head_dim) out[d] = from_f32<T>(acc[e] * inv);
+  }
+}
+
 // Log-sum-exp merge of a row's split partials, one wave per (row, q head),
-// 4 waves per workgroup. Lane s holds split s's weight; each lane owns ND
-// dims and issues the loads of all splits at once.
+// 4 waves per workgroup.
 template <typename T, int ND>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   const int lane = threadIdx.x & 63;
@@ -325,40 +383,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   if (n <= 0) return;
   const Partition P = partition(n, a);
   if (P.nsplit <= 1) return;
-  const int64_t idx0 = (row * a.q_heads + head) * kMaxSplits;
-  const bool live = lane < P.nsplit;
-  const float mi = live ? a.part_ml[(idx0 + lane) * 2 + 0] : -INFINITY;
-  const float li = live ? a.part_ml[(idx0 + lane) * 2 + 1] : 0.f;
-  const float M = wave_max(mi);
-  const float wi = live ? fast_exp2(mi - M) : 0.f;
-  const float L = wave_sum(wi * li);
-  const float inv = fast_rcp(fmaxf(L, 1e-30f));
-  const float* part = a.part_acc + idx0 * a.head_dim;
-  float acc[ND];
-#pragma unroll
-  for (int e = 0; e < ND; ++e) acc[e] = 0.f;
-  // Every split's partial row is loaded at once (they do not depend on the
-  // weights), then combined in split order.
-  float v[kMaxSplits][ND];
-#pragma unroll
-  for (int j = 0; j < kMaxSplits; ++j)
-#pragma unroll
-    for (int e = 0; e < ND; ++e) {
-      const int d = lane + 64 * e;
-      v[j][e] = (j < P.nsplit && d < a.head_dim) ? part[(int64_t)j * a.head_dim + d] : 0.f;
-    }
-#pragma unroll
-  for (int j = 0; j < kMaxSplits; ++j) {
-    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wi), j));
-#pragma unroll
-    for (int e = 0; e < ND; ++e) acc[e] = fmaf(w, v[j][e], acc[e]);
-  }
-  T* out = reinterpret_cast<T*>(a.out) + qrow * a.o_row + (int64_t)head * a.o_head;
-#pragma unroll
-  for (int e = 0; e < ND; ++e) {
-    const int d = lane + 64 * e;
-    if (d < a.head_dim) out[d] = from_f32<T>(acc[e] * inv);
-  }
+  merge_partials<T, ND>(a, row, head, qrow, P.nsplit, lane, 0);
 }
 
 template <typename T>
@@ -377,8 +402,8 @@ void launch_merge(int head_dim, dim3 grid, hipStream_t s, const DecodeArgs& a) {
 template <typename T, int VEC>
 bool launch_vec(int lpt, dim3 grid, dim3 block, hipStream_t s, const DecodeArgs& a) {
   switch (lpt) {
-#define VRH_LPT(L)                                                                      \
-  case L:                                                                               \
+#define VRH_LPT(L)                                                              \
+  case L:                                                                       \
     hipLaunchKernelGGL((paged_decode_kernel<T, VEC, L>), grid, block, 0, s, a); \
     return true;
     VRH_LPT(1)
@@ -410,6 +435,7 @@ bool launch_decode(int vec, int lpt, dim3 grid, dim3 block, hipStream_t s, const
 }  // namespace vrh
 
 using namespace vrh;
+
 
 extern "C" size_t vrh_paged_decode_workspace_bytes(int64_t rows, int32_t q_heads,
                                                    int32_t head_dim) {
