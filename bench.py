@@ -59,7 +59,7 @@ def parse_args():
                         help="budget of the CPU baseline sample")
     parser.add_argument("--leg", choices=["prefill_config4", "prefill_chunks_config4",
                                           "append_config4", "decode_config2",
-                                          "decode_config5"],
+                                          "decode_config5", "decode_gqa"],
                         help="run only this workload (for profiling) and print its timing")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run vrh_kv_copy_blocks over a known byte count (the "
@@ -500,6 +500,28 @@ def decode_config5_leg(device, calls=6):
     return out
 
 
+def decode_gqa_leg(device, calls=8):
+    """Grouped-query decode: config 2's 64 rows and context range with 32 q
+    heads over 8 kv heads (head_dim 128, bf16). Algorithmic bytes count each
+    K/V byte once per row (what one wave per kv head group reads)."""
+    import torch
+
+    from vllm_rlt import workloads
+    from vllm_rlt.kernels.hip_attention import paged_attention
+
+    w = workloads.gqa_decode(device=device)
+    kc, vc = w.key_cache[:, 0], w.value_cache[:, 0]
+    call = lambda: paged_attention(w.q, kc, vc, w.block_tables, w.context_lengths)  # noqa: E731
+    ms = graph_time_ms([call] * calls, replays=4)
+    nbytes = w.decode_bytes()
+    out = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 2), "us": round(ms * 1e3, 2),
+           "pct_of_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+           "bytes_per_call": nbytes, "rows": w.rows, "q_heads": 32, "kv_heads": 8}
+    del w, kc, vc
+    torch.cuda.empty_cache()
+    return out
+
+
 def single_leg(name, repeats):
     """One workload alone, for rocprofv3 runs (kernel durations and counters of
     that workload only)."""
@@ -537,6 +559,8 @@ def single_leg(name, repeats):
         nbytes = w.decode_bytes()
         print(json.dumps({"leg": name, "us": round(ms * 1e3, 2), "bytes_per_call": nbytes,
                           "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2)}), flush=True)
+    elif name == "decode_gqa":
+        print(json.dumps({"leg": name, **decode_gqa_leg(device, calls=repeats)}), flush=True)
     elif name == "decode_config5":
         print(json.dumps({"leg": name, **decode_config5_leg(device, calls=repeats)}),
               flush=True)
@@ -730,6 +754,7 @@ def main():
         print(f"bench: {torch.cuda.memory_allocated() / 2**30:.1f} GiB held before the "
               "192 GiB config-5 pool", file=sys.stderr, flush=True)
         extras["decode_config5_long_context"] = decode_config5_leg(device)
+        extras["decode_gqa_32q_8kv"] = decode_gqa_leg(device)
         pw = workloads.config4(device=device)
         kc, vc = pw.key_cache[:, 0], pw.value_cache[:, 0]
         fns, append_bytes, keep, append_rows = rotating_append_config4(pw)

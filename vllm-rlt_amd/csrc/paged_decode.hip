@@ -5,8 +5,11 @@
 // own block table, GQA head h reads kv head h / G, scores scaled by 1/sqrt(D),
 // fp32 softmax, output rounded to the storage dtype, zero rows for length 0.
 //
-// Design (bandwidth-bound; every K/V byte is read exactly once per q head):
-//  * One 64-lane wavefront per (split, q head, row). A split is a run of whole
+// Design (bandwidth-bound; every K/V byte is read once per group of up to 8
+// q heads that share its kv head):
+//  * One 64-lane wavefront per (split, group of HPW q heads, row): HPW = 8, 4
+//    or 2 grouped-query heads when they divide the group (each loaded K/V
+//    vector serves all of them), else 1. A split is a run of whole
 //    pages: bps = max(min_bps, ceil(pages / kMaxSplits)) pages (at least 128
 //    tokens, at most 16 splits per row), so the partition depends only on
 //    the row's own length -> batch invariance. The split index is rotated
@@ -48,6 +51,9 @@ namespace {
 #define VRH_DECODE_PREFETCH 1
 #endif
 
+#ifndef VRH_DECODE_MAX_HPW
+#define VRH_DECODE_MAX_HPW 8  // grouped-query heads one wave may serve
+#endif
 #ifndef VRH_MAX_SPLITS
 #define VRH_MAX_SPLITS 16
 #endif
@@ -152,49 +158,54 @@ __device__ __forceinline__ int row_length(int64_t row, const DecodeArgs& a, int6
   return clamp_length(a.lengths[seq] - q_len + i + 1, a);
 }
 
-// The work of one (row, q head) over splits split0, split0 + step, ... of
-// the row's partition: multi-split rows write (m, l, acc) partials, single
-// splits the output; a zero-length row writes zeros (from split 0).
-template <typename T, int VEC, int LPT>
-__device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, int head,
+// The work of one row and HPW consecutive q heads of one kv head (the
+// grouped-query heads that share it) over splits split0, split0 + step, ...
+// of the row's partition: each K/V vector a lane loads serves all HPW heads.
+// Multi-split rows write (m, l, acc) partials, single splits the output; a
+// zero-length row writes zeros (from split 0).
+template <typename T, int VEC, int LPT, int HPW>
+__device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, int head0,
                                             int split0, int step) {
+  constexpr int U = HPW >= 4 ? (kU > 2 ? kU / 2 : kU) : kU;  // loads per chunk
   constexpr int TPL = 64 / LPT;  // tokens per wave load
-  constexpr int CH = kU * TPL;   // tokens per chunk
+  constexpr int CH = U * TPL;    // tokens per chunk
   using raw_t = typename Vec<T, VEC>::raw_t;
 
   const int lane = threadIdx.x & 63;
   const int dg = lane % LPT;
   const int tg = lane / LPT;
-  const int kvh = head / a.group;
+  const int kvh = head0 / a.group;
   int64_t trow, qrow;
   const int n = row_length(row, a, &trow, &qrow);
   if (n < 0) return;
   const bool dvalid = dg * VEC < a.head_dim;
-  T* out = reinterpret_cast<T*>(a.out) + qrow * a.o_row + (int64_t)head * a.o_head + dg * VEC;
+  T* out = reinterpret_cast<T*>(a.out) + qrow * a.o_row + (int64_t)head0 * a.o_head + dg * VEC;
 
   if (n == 0) {
     if (split0 == 0 && tg == 0 && dvalid) {
       float z[VEC];
 #pragma unroll
       for (int i = 0; i < VEC; ++i) z[i] = 0.f;
-      store_raw<T, VEC>(out, pack<T, VEC>(z));
+#pragma unroll
+      for (int h = 0; h < HPW; ++h) store_raw<T, VEC>(out + h * a.o_head, pack<T, VEC>(z));
     }
     return;
   }
   const Partition P = partition(n, a);
   if (split0 >= P.nsplit) return;
-  float qf[VEC];
-  {
-    const T* qp = reinterpret_cast<const T*>(a.q) + qrow * a.q_row + (int64_t)head * a.q_head +
-                  dg * VEC;
+  float qf[HPW][VEC];
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) {
+    const T* qp = reinterpret_cast<const T*>(a.q) + qrow * a.q_row +
+                  (int64_t)(head0 + h) * a.q_head + dg * VEC;
     if (dvalid) {
-      unpack<T, VEC>(load_raw<T, VEC>(qp), qf);
+      unpack<T, VEC>(load_raw<T, VEC>(qp), qf[h]);
     } else {
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) qf[i] = 0.f;
+      for (int i = 0; i < VEC; ++i) qf[h][i] = 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) qf[i] *= a.scale_log2;
+    for (int i = 0; i < VEC; ++i) qf[h][i] *= a.scale_log2;
   }
   // Lanes past head_dim read dims [0, VEC) instead (in bounds); their q is zero
   // and they store nothing.
@@ -209,10 +220,15 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
     const int tb = max(P.start, b0 * a.block_size);
     const int te = min(n, b1 * a.block_size);
 
-    float m = -INFINITY, l = 0.f;
-    float acc[VEC];
+    float m[HPW], l[HPW];
+    float acc[HPW][VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
+    for (int h = 0; h < HPW; ++h) {
+      m[h] = -INFINITY;
+      l[h] = 0.f;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[h][i] = 0.f;
+    }
 
     for (int seg = b0; seg < b1; seg += 64) {
       const int tbl = (seg + lane < b1) ? table[seg + lane] : 0;
@@ -221,9 +237,9 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
       if (s_tb >= s_te) continue;
       // Branch-free loads: positions past the end re-read the last valid token
       // (masked out of the softmax), so a chunk is one straight run of loads.
-      auto issue = [&](int p0, raw_t (&kr)[kU], raw_t (&vr)[kU]) {
+      auto issue = [&](int p0, raw_t (&kr)[U], raw_t (&vr)[U]) {
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
+        for (int u = 0; u < U; ++u) {
           const int pos = min(p0 + u * TPL + tg, s_te - 1);
           int page, off;
           if (a.bs_shift >= 0) {
@@ -238,44 +254,58 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
           vr[u] = load_kv<T, VEC>(vbase + blk * a.v_block + (int64_t)off * a.v_token);
         }
       };
-      raw_t kr[kU], vr[kU];
+      raw_t kr[U], vr[U];
       issue(s_tb, kr, vr);
       for (int p0 = s_tb; p0 < s_te; p0 += CH) {
 #if VRH_DECODE_PREFETCH
-        raw_t kn[kU], vn[kU];
+        raw_t kn[U], vn[U];
         if (p0 + CH < s_te) issue(p0 + CH, kn, vn);
 #endif
-        float s[kU];
-        float mx = m;
+        float sc[HPW][U];
+        float mx[HPW];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
+        for (int h = 0; h < HPW; ++h) mx[h] = m[h];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
           float kf[VEC];
           unpack<T, VEC>(kr[u], kf);
-          float d = 0.f;
+          const bool visible = p0 + u * TPL + tg < s_te;
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) d = fmaf(qf[i], kf[i], d);
-          d = group_sum<LPT>(d);
-          s[u] = (p0 + u * TPL + tg < s_te) ? d : -INFINITY;
-          mx = fmaxf(mx, s[u]);
+          for (int h = 0; h < HPW; ++h) {
+            float d = 0.f;
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) d = fmaf(qf[h][i], kf[i], d);
+            d = group_sum<LPT>(d);
+            sc[h][u] = visible ? d : -INFINITY;
+            mx[h] = fmaxf(mx[h], sc[h][u]);
+          }
         }
-        const float safe = (mx == -INFINITY) ? 0.f : mx;
-        const float corr = fast_exp2(m - safe);
-        l *= corr;
+        float safe[HPW];
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[i] *= corr;
+        for (int h = 0; h < HPW; ++h) {
+          safe[h] = (mx[h] == -INFINITY) ? 0.f : mx[h];
+          const float corr = fast_exp2(m[h] - safe[h]);
+          l[h] *= corr;
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-          const float p = fast_exp2(s[u] - safe);
-          l += p;
+          for (int i = 0; i < VEC; ++i) acc[h][i] *= corr;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
           float vf[VEC];
           unpack<T, VEC>(vr[u], vf);
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) acc[i] = fmaf(p, vf[i], acc[i]);
+          for (int h = 0; h < HPW; ++h) {
+            const float p = fast_exp2(sc[h][u] - safe[h]);
+            l[h] += p;
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) acc[h][i] = fmaf(p, vf[i], acc[h][i]);
+          }
         }
-        m = mx;
+#pragma unroll
+        for (int h = 0; h < HPW; ++h) m[h] = mx[h];
 #if VRH_DECODE_PREFETCH
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
+        for (int u = 0; u < U; ++u) {
           kr[u] = kn[u];
           vr[u] = vn[u];
         }
@@ -285,40 +315,43 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
       }
     }
 
-    // Merge the token groups' states (fixed butterfly order).
-    const float M = cross_group_max<LPT>(m);
-    const float w = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
-    const float L = cross_group_sum<LPT>(l * w);
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) acc[i] = cross_group_sum<LPT>(acc[i] * w);
+    for (int h = 0; h < HPW; ++h) {
+      // Merge the token groups' states (fixed butterfly order).
+      const float M = cross_group_max<LPT>(m[h]);
+      const float w = (m[h] == -INFINITY) ? 0.f : fast_exp2(m[h] - M);
+      const float L = cross_group_sum<LPT>(l[h] * w);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[h][i] = cross_group_sum<LPT>(acc[h][i] * w);
 
-    if (P.nsplit == 1) {
-      if (tg == 0 && dvalid) {
-        const float inv = fast_rcp(fmaxf(L, 1e-30f));
-        float o[VEC];
+      if (P.nsplit == 1) {
+        if (tg == 0 && dvalid) {
+          const float inv = fast_rcp(fmaxf(L, 1e-30f));
+          float o[VEC];
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) o[i] = acc[i] * inv;
-        store_raw<T, VEC>(out, pack<T, VEC>(o));
-      }
-    } else {
-      const int64_t idx = ((row * a.q_heads + head) * kMaxSplits) + split;
-      if (lane == 0) {
-        a.part_ml[idx * 2 + 0] = M;
-        a.part_ml[idx * 2 + 1] = L;
-      }
-      if (tg == 0 && dvalid) {
-        float* dst = a.part_acc + idx * a.head_dim + dg * VEC;
+          for (int i = 0; i < VEC; ++i) o[i] = acc[h][i] * inv;
+          store_raw<T, VEC>(out + h * a.o_head, pack<T, VEC>(o));
+        }
+      } else {
+        const int64_t idx = ((row * a.q_heads + head0 + h) * kMaxSplits) + split;
+        if (lane == 0) {
+          a.part_ml[idx * 2 + 0] = M;
+          a.part_ml[idx * 2 + 1] = L;
+        }
+        if (tg == 0 && dvalid) {
+          float* dst = a.part_acc + idx * a.head_dim + dg * VEC;
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) dst[i] = acc[i];
+          for (int i = 0; i < VEC; ++i) dst[i] = acc[h][i];
+        }
       }
     }
   }
 }
 
-// Grid form: one wave per (split column, q head, row).
-template <typename T, int VEC, int LPT>
+// Grid form: one wave per (split column, group of HPW q heads, row).
+template <typename T, int VEC, int LPT, int HPW>
 __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
-  const int head = blockIdx.y;
+  const int head = blockIdx.y * HPW;
   const int64_t row = a.row_base + blockIdx.z;
   // Workgroup L = x + gx * (head + heads * row) runs on XCD L % 8. Rows need
   // different split counts, so with split = x the low split indices (present
@@ -326,7 +359,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   // (head + heads * row) spreads every split position evenly over the XCDs.
   int split0 = (int)blockIdx.x - (int)((blockIdx.y + (int64_t)gridDim.y * blockIdx.z) % gridDim.x);
   if (split0 < 0) split0 += gridDim.x;
-  decode_work<T, VEC, LPT>(a, row, head, split0, gridDim.x);
+  decode_work<T, VEC, LPT, HPW>(a, row, head, split0, gridDim.x);
 }
 
 // Log-sum-exp merge of one (row, q head)'s split partials by one wave, for
@@ -399,13 +432,32 @@ void launch_merge(int head_dim, dim3 grid, hipStream_t s, const DecodeArgs& a) {
   }
 }
 
+template <typename T, int VEC, int LPT>
+bool launch_hpw(int hpw, dim3 grid, hipStream_t s, const DecodeArgs& a) {
+  switch (hpw) {
+    case 1: hipLaunchKernelGGL((paged_decode_kernel<T, VEC, LPT, 1>), grid, dim3(64), 0, s, a); return true;
+    case 2: hipLaunchKernelGGL((paged_decode_kernel<T, VEC, LPT, 2>), grid, dim3(64), 0, s, a); return true;
+    case 4: hipLaunchKernelGGL((paged_decode_kernel<T, VEC, LPT, 4>), grid, dim3(64), 0, s, a); return true;
+    case 8: hipLaunchKernelGGL((paged_decode_kernel<T, VEC, LPT, 8>), grid, dim3(64), 0, s, a); return true;
+    default: return false;
+  }
+}
+
+// Instantiations: every (VEC, LPT) for one head per wave; grouped heads per
+// wave (HPW > 1) only for full-width lanes of the usual head dims
+// (16-byte vectors, LPT 4, 8 or 16: head_dim 32, 64, 128 in 16-bit types).
 template <typename T, int VEC>
-bool launch_vec(int lpt, dim3 grid, dim3 block, hipStream_t s, const DecodeArgs& a) {
+bool launch_vec(int lpt, int hpw, dim3 grid, hipStream_t s, const DecodeArgs& a) {
+  constexpr bool kWide = VEC * (int)sizeof(T) == 16;
   switch (lpt) {
-#define VRH_LPT(L)                                                              \
-  case L:                                                                       \
-    hipLaunchKernelGGL((paged_decode_kernel<T, VEC, L>), grid, block, 0, s, a); \
-    return true;
+#define VRH_LPT(L)                                                                 \
+  case L:                                                                          \
+    if (hpw == 1) {                                                                \
+      hipLaunchKernelGGL((paged_decode_kernel<T, VEC, L, 1>), grid, dim3(64), 0, s, a); \
+      return true;                                                                 \
+    }                                                                              \
+    if constexpr (kWide && L >= 4 && L <= 16) return launch_hpw<T, VEC, L>(hpw, grid, s, a); \
+    return false;
     VRH_LPT(1)
     VRH_LPT(2)
     VRH_LPT(4)
@@ -419,13 +471,13 @@ bool launch_vec(int lpt, dim3 grid, dim3 block, hipStream_t s, const DecodeArgs&
 }
 
 template <typename T>
-bool launch_decode(int vec, int lpt, dim3 grid, dim3 block, hipStream_t s, const DecodeArgs& a) {
+bool launch_decode(int vec, int lpt, int hpw, dim3 grid, hipStream_t s, const DecodeArgs& a) {
   switch (vec) {
-    case 1: return launch_vec<T, 1>(lpt, grid, block, s, a);
-    case 2: return launch_vec<T, 2>(lpt, grid, block, s, a);
-    case 4: return launch_vec<T, 4>(lpt, grid, block, s, a);
+    case 1: return launch_vec<T, 1>(lpt, hpw, grid, s, a);
+    case 2: return launch_vec<T, 2>(lpt, hpw, grid, s, a);
+    case 4: return launch_vec<T, 4>(lpt, hpw, grid, s, a);
     case 8:
-      if constexpr (sizeof(T) == 2) return launch_vec<T, 8>(lpt, grid, block, s, a);
+      if constexpr (sizeof(T) == 2) return launch_vec<T, 8>(lpt, hpw, grid, s, a);
       return false;
     default: return false;
   }
@@ -538,6 +590,15 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
   a.min_bps = workspace != nullptr ? std::max(1, kSplitTokens / block_size)
                                    : std::max(1, table_width);
 
+  // Grouped-query heads per wave: the largest of 8, 4, 2 dividing the group
+  // (1 without grouping, or where no grouped instantiation exists).
+  int hpw = 1;
+  if (vec * es == 16 && lpt >= 4 && lpt <= 16)
+    for (int h : {8, 4, 2})
+      if (a.group % h == 0 && h <= VRH_DECODE_MAX_HPW) {
+        hpw = h;
+        break;
+      }
   // Largest split count any row of this table width can need: the grid is a
   // function of shapes only (graph capture), never of device lengths.
   const int max_pages = std::max(1, table_width);
@@ -546,14 +607,13 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
     a.row_base = first;
     const unsigned count = (unsigned)std::min<int64_t>(rows - first, 65535);
     bool ok = false;
-    dim3 grid((unsigned)gx, (unsigned)q_heads, count);
-    dim3 block(64);
+    dim3 grid((unsigned)gx, (unsigned)(q_heads / hpw), count);
     switch (dtype) {
-      case VRH_DTYPE_F32: ok = launch_decode<float>(vec, lpt, grid, block, s, a); break;
-      case VRH_DTYPE_F16: ok = launch_decode<f16_t>(vec, lpt, grid, block, s, a); break;
-      case VRH_DTYPE_BF16: ok = launch_decode<bf16_t>(vec, lpt, grid, block, s, a); break;
+      case VRH_DTYPE_F32: ok = launch_decode<float>(vec, lpt, hpw, grid, s, a); break;
+      case VRH_DTYPE_F16: ok = launch_decode<f16_t>(vec, lpt, hpw, grid, s, a); break;
+      case VRH_DTYPE_BF16: ok = launch_decode<bf16_t>(vec, lpt, hpw, grid, s, a); break;
     }
-    VRH_CHECK_ARG(ok, "%s: no kernel for vec=%d lanes=%d", who, vec, lpt);
+    VRH_CHECK_ARG(ok, "%s: no kernel for vec=%d lanes=%d heads/wave=%d", who, vec, lpt, hpw);
     if (gx == 1) continue;  // every row is a single split: output already written
     dim3 mgrid((unsigned)ceil_div(q_heads, 4), count);
     switch (dtype) {

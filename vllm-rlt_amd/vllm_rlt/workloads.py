@@ -238,6 +238,28 @@ def config5(device="cpu", rows=256, ctx_low=2048, ctx_high=32768, layers=48,
                           wb.to(device), wo.to(device))
 
 
+def gqa_decode(device="cpu", rows=64, q_heads=32, kv_heads=8, ctx_low=512, ctx_high=4096,
+               dtype=torch.bfloat16) -> DecodeWorkload:
+    """Grouped-query decode (q_heads / kv_heads q heads per kv head) at config 2's
+    row count and context range, over a one-layer pool of the rows' pages."""
+    g_tab, g_val, g_len = _gens()
+    lengths = _randint(g_len, ctx_low, ctx_high, rows) + 1
+    pages = ((lengths + BLOCK - 1) // BLOCK).tolist()
+    num_blocks = sum(pages)
+    tables = _scatter_pages(g_tab, pages, num_blocks)
+    shape = (num_blocks, 1, BLOCK, kv_heads, HEAD_DIM)
+    key_cache = torch.empty(shape, dtype=dtype, device=device)
+    value_cache = torch.empty_like(key_cache)
+    _fill_pool(key_cache, g_val, 0.5)
+    _fill_pool(value_cache, g_val, 0.5)
+    q = _values(g_val, (rows, q_heads, HEAD_DIM), dtype, 0.5, device)
+    empty = torch.empty((1, 0, kv_heads, HEAD_DIM), dtype=dtype, device=device)
+    none = torch.empty(0, dtype=torch.int64, device=device)
+    return DecodeWorkload("gqa", dtype, 1, num_blocks, key_cache, value_cache, q, empty, empty,
+                          _table_tensor(tables, max(pages)).to(device),
+                          lengths.to(torch.int32).to(device), none, none)
+
+
 @dataclass
 class PrefillWorkload:
     """Packed WCPB chunks + decode rows of config 4 (one layer)."""
