@@ -39,7 +39,7 @@ namespace {
 // each of K and V), minimum split length, next-chunk prefetch, non-temporal
 // K/V loads.
 #ifndef VRH_DECODE_U
-#define VRH_DECODE_U 4
+#define VRH_DECODE_U 8
 #endif
 #ifndef VRH_SPLIT_TOKENS
 #define VRH_SPLIT_TOKENS 128
@@ -48,7 +48,7 @@ namespace {
 #define VRH_DECODE_NT 1
 #endif
 #ifndef VRH_DECODE_PREFETCH
-#define VRH_DECODE_PREFETCH 1
+#define VRH_DECODE_PREFETCH 0
 #endif
 
 #ifndef VRH_DECODE_MAX_HPW
@@ -166,7 +166,8 @@ __device__ __forceinline__ int row_length(int64_t row, const DecodeArgs& a, int6
 template <typename T, int VEC, int LPT, int HPW>
 __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, int head0,
                                             int split0, int step) {
-  constexpr int U = HPW >= 4 ? (kU > 2 ? kU / 2 : kU) : kU;  // loads per chunk
+  // Loads per chunk: fewer when many heads' state shares the registers.
+  constexpr int U = (2 * kU / HPW) < 1 ? 1 : ((2 * kU / HPW) > kU ? kU : 2 * kU / HPW);
   constexpr int TPL = 64 / LPT;  // tokens per wave load
   constexpr int CH = U * TPL;    // tokens per chunk
   using raw_t = typename Vec<T, VEC>::raw_t;
