@@ -100,6 +100,7 @@ struct PrefillArgs {
   int32_t group, block_size, bs_shift, table_width;
   int32_t skip_q;  // sequences with q_len <= skip_q are left to the decode kernel
   int32_t uniform_pages;  // block size a power-of-two multiple of 256 / (16-byte chunks per row)
+  int32_t same_kv32;      // K and V block/token strides equal and below 2^31
   const int32_t* order;   // sequences in dispatch order (longest first), or null
   float scale_log2;
 };
@@ -141,6 +142,9 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
+#ifndef VRH_PREFILL_SAME_KV32
+#define VRH_PREFILL_SAME_KV32 1
+#endif
 #ifndef VRH_PREFILL_WG_PER_CU
 #define VRH_PREFILL_WG_PER_CU 2
 #endif
@@ -268,6 +272,23 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
       if (last_page >= tbl_base + kTableSeg) load_table(page_of(k0));
     }
     auto pad = [&](int inst) { return SB_INST % kWaves != 0 && inst >= SB_INST; };
+    if (kPow2 && a.uniform_pages && a.same_kv32 && k0 + kSB <= end) {
+      // K and V share block / token strides below 2^31 elements: one 32 x 32
+      // -> 64-bit scalar product per instruction addresses both.
+#pragma unroll
+      for (int r = 0; r < NI; ++r) {
+        const int inst = wave + kWaves * r;
+        if (pad(inst)) continue;
+        const int pb = k0 + r * S;
+        const uint32_t page = __builtin_amdgcn_readfirstlane(tbl_lds[(pb >> a.bs_shift) - tbl_base]);
+        const uint32_t row_off = pb & (a.block_size - 1);
+        const uint64_t off = (uint64_t)page * (uint32_t)a.k_block +
+                             (uint64_t)row_off * (uint32_t)a.k_token;
+        R.k[r] = *reinterpret_cast<const u32x4*>(lane_k + off);
+        R.v[r] = *reinterpret_cast<const u32x4*>(lane_v + off);
+      }
+      return;
+    }
     if (kPow2 && a.uniform_pages && k0 + kSB <= end) {
 #pragma unroll
       for (int r = 0; r < NI; ++r) {
@@ -683,6 +704,10 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
     const bool pow2_chunks = (chunks & (chunks - 1)) == 0;
     a.uniform_pages = pow2_chunks && a.bs_shift >= 0 && block_size % (256 / chunks) == 0;
   }
+  a.same_kv32 = VRH_PREFILL_SAME_KV32 && k_block_stride == v_block_stride &&
+                k_token_stride == v_token_stride && k_block_stride >= 0 &&
+                k_block_stride < (1ll << 31) && k_token_stride >= 0 &&
+                k_token_stride < (1ll << 31);
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
   a.num_seqs = num_seqs;
   a.kv_heads = kv_heads;
