@@ -59,7 +59,7 @@ def parse_args():
                         help="budget of the CPU baseline sample")
     parser.add_argument("--leg", choices=["prefill_config4", "prefill_chunks_config4",
                                           "append_config4", "decode_config2",
-                                          "decode_config5", "decode_gqa"],
+                                          "decode_config5", "decode_gqa", "movers"],
                         help="run only this workload (for profiling) and print its timing")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run vrh_kv_copy_blocks over a known byte count (the "
@@ -319,14 +319,21 @@ def mlp_and_rows_extras(device, chunk_rows):
         out[name] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 2), "us": round(ms * 1e3, 2),
                      "pct_of_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
         del gate, up
+    # Hidden-state segments: 4 disjoint sets of pool rows and batch buffers
+    # (268 MB in all), rotated so that no call re-reads the previous ones'.
     hidden = 2048
     slots, pool_rows = 64, 1024
     pool = torch.randn(slots * pool_rows, hidden, generator=gen).to(torch.bfloat16).to(device)
-    seg = [[(7 * i) % slots, 512 * (i % 2), 512, 512 * i, 1] for i in range(chunk_rows // 512)]
-    segments = torch.tensor(seg, dtype=torch.int64, device=device)
-    batch = torch.empty(chunk_rows, hidden, dtype=torch.bfloat16, device=device)
-    g_ms = graph_time_ms([lambda: gather_segments(pool, segments, batch, pool_rows, 512)] * 16)
-    s_ms = graph_time_ms([lambda: scatter_segments(batch, segments, pool, pool_rows, 512)] * 16)
+    segment_sets, batches = [], []
+    for k in range(4):
+        seg = [[(7 * i + 16 * k) % slots, 512 * (i % 2), 512, 512 * i, 1]
+               for i in range(chunk_rows // 512)]
+        segment_sets.append(torch.tensor(seg, dtype=torch.int64, device=device))
+        batches.append(torch.empty(chunk_rows, hidden, dtype=torch.bfloat16, device=device))
+    g_ms = graph_time_ms([lambda k=k: gather_segments(pool, segment_sets[k], batches[k], pool_rows,
+                                                      512) for k in range(4)] * 4)
+    s_ms = graph_time_ms([lambda k=k: scatter_segments(batches[k], segment_sets[k], pool,
+                                                       pool_rows, 512) for k in range(4)] * 4)
     nbytes = chunk_rows * hidden * 2 * 2
     for name, ms in (("gather_segments_config4", g_ms), ("scatter_segments_config4", s_ms)):
         out[name] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 2), "us": round(ms * 1e3, 2),
@@ -376,11 +383,13 @@ def metadata_extras(device):
     out["routing_metadata_64_rows_us"] = round(meta_ms * 1e3, 2)
     out["routing_slots_64_rows_us"] = round(slots_ms * 1e3, 2)
     out["expand_kv_addresses_8039_us"] = round(expand_ms * 1e3, 2)
-    # read (kv_gather) of a 4096-token request from a 24-layer pool layer view
-    pool = torch.randn((300, 24, 16, 16, 128), generator=gen).to(torch.bfloat16).to(device)
-    table = torch.randperm(300, generator=gen)[:256].to(torch.int32).to(device)
+    # read (kv_gather) of a 4096-token request from a 24-layer pool layer
+    # view, rotating over 4 requests with disjoint pages
+    pool = torch.empty((1100, 24, 16, 16, 128), dtype=torch.bfloat16, device=device).normal_()
+    tables = torch.randperm(1100, generator=gen)[:1024].to(torch.int32).to(device).view(4, 256)
     kview, vview = pool[:, 5], pool[:, 7]
-    gather_ms = graph_time_ms([lambda: kv_gather(kview, vview, table, 4096)] * 8)
+    gather_ms = graph_time_ms([lambda k=k: kv_gather(kview, vview, tables[k], 4096)
+                               for k in range(4)] * 2)
     gbytes = 4096 * 16 * 128 * 2 * 2 * 2
     out["kv_gather_4096_tokens"] = {"gbs": round(gbytes / (gather_ms * 1e-3) / 1e9, 2),
                                     "us": round(gather_ms * 1e3, 2)}
@@ -522,6 +531,48 @@ def decode_gqa_leg(device, calls=8):
     return out
 
 
+def pool_movers(work, replays=2):
+    """Whole-block copy and LAST_EXITED finalize on the config-2 pool, each over
+    16 disjoint sets so that no call re-reads bytes a previous one touched.
+    copy: 64 random 3 MiB blocks (K and V) per call; finalize: the 64 rows'
+    tokens at 16 different positions, from their depth plane into every
+    deeper plane, all 24 layers."""
+    import torch
+
+    from vllm_rlt.kernels.hip_attention import kv_copy_blocks, kv_finalize
+
+    device = work.key_cache.device
+    layers = work.layers
+    gen = torch.Generator().manual_seed(5)
+    perm = torch.randperm(work.num_blocks, generator=gen)[: 128 * 16].to(device).view(16, 128)
+    copy_ms = graph_time_ms(
+        [lambda i=i: kv_copy_blocks(work.key_cache, work.value_cache, perm[i, :64],
+                                    perm[i, 64:]) for i in range(16)], replays=replays)
+    block_bytes = work.key_cache[0].numel() * work.key_cache.element_size()
+    copy_bytes = 64 * block_bytes * 2 * 2
+    depths = work.extra["depths"]
+    planes = 4
+    plane_tables = work.extra["plane_tables"]
+    width = max(len(t) for t in plane_tables)
+    table_dev = torch.zeros((len(plane_tables), width), dtype=torch.int32)
+    for i, pages in enumerate(plane_tables):
+        table_dev[i, : len(pages)] = torch.tensor(pages, dtype=torch.int32)
+    table_dev = table_dev.to(device)
+    last = (work.context_lengths - 1).to(torch.int64).cpu()
+    descs = [torch.stack([torch.arange(work.rows), depths.to(torch.int64), last - k], 1).to(device)
+             for k in range(16)]
+    fin_ms = graph_time_ms(
+        [lambda d=d: kv_finalize(work.key_cache, work.value_cache, d, table_dev, planes)
+         for d in descs], replays=replays)
+    slot = work.key_cache.shape[3] * work.key_cache.shape[4] * work.key_cache.element_size()
+    fin_bytes = int((planes - 1 - depths).sum()) * layers * slot * 2 * 2
+    return {"copy_blocks_64x3MiB": {"gbs": round(copy_bytes / (copy_ms * 1e-3) / 1e9, 2),
+                                    "us": round(copy_ms * 1e3, 2), "bytes": copy_bytes},
+            "finalize_64_tokens_24_layers": {"gbs": round(fin_bytes / (fin_ms * 1e-3) / 1e9, 2),
+                                             "us": round(fin_ms * 1e3, 2), "bytes": fin_bytes,
+                                             "rotation": "16 token positions per row"}}
+
+
 def single_leg(name, repeats):
     """One workload alone, for rocprofv3 runs (kernel durations and counters of
     that workload only)."""
@@ -559,6 +610,15 @@ def single_leg(name, repeats):
         nbytes = w.decode_bytes()
         print(json.dumps({"leg": name, "us": round(ms * 1e3, 2), "bytes_per_call": nbytes,
                           "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2)}), flush=True)
+    elif name == "movers":
+        # every byte mover of the path once per replay, for counter runs
+        w = workloads.config2(device=device)
+        out = pool_movers(w, replays=repeats)
+        del w
+        torch.cuda.empty_cache()
+        out.update(mlp_and_rows_extras(device, 8192))
+        out.update(metadata_extras(device))
+        print(json.dumps({"leg": name, **out}), flush=True)
     elif name == "decode_gqa":
         print(json.dumps({"leg": name, **decode_gqa_leg(device, calls=repeats)}), flush=True)
     elif name == "decode_config5":
@@ -585,8 +645,6 @@ def main():
     from vllm_rlt.kernels.hip_attention import (
         kv_append,
         kv_append_layers,
-        kv_copy_blocks,
-        kv_finalize,
         paged_attention,
         paged_prefill_attention,
     )
@@ -705,36 +763,7 @@ def main():
                 "rotation": "48 disjoint input/destination sets, 1.2 GB"},
             "append_one_layer_us": round(single_ms * 1e3, 2),
             "append_one_layer_gbs": round(work.append_bytes(1) / (single_ms * 1e-3) / 1e9, 2)}
-        # Whole-block copy (copy-on-write / compaction): 64 random 3 MiB blocks
-        # per call, a different set each call (no cache can serve the repeats).
-        gen = torch.Generator().manual_seed(5)
-        perm = torch.randperm(work.num_blocks, generator=gen)[: 128 * 16].to(device).view(16, 128)
-        copy_ms = graph_time_ms(
-            [lambda i=i: kv_copy_blocks(work.key_cache, work.value_cache, perm[i, :64],
-                                        perm[i, 64:]) for i in range(16)], replays=2)
-        block_bytes = work.key_cache[0].numel() * work.key_cache.element_size()
-        copy_bytes = 64 * block_bytes * 2 * 2
-        extras["copy_blocks_64x3MiB"] = {
-            "gbs": round(copy_bytes / (copy_ms * 1e-3) / 1e9, 2), "us": round(copy_ms * 1e3, 2)}
-        # LAST_EXITED finalize of the step's 64 tokens from their depth into
-        # every deeper plane, all 24 layers (device descriptors).
-        depths = work.extra["depths"]
-        planes = 4
-        plane_tables = work.extra["plane_tables"]
-        width = max(len(t) for t in plane_tables)
-        table_dev = torch.zeros((len(plane_tables), width), dtype=torch.int32)
-        for i, pages in enumerate(plane_tables):
-            table_dev[i, : len(pages)] = torch.tensor(pages, dtype=torch.int32)
-        table_dev = table_dev.to(device)
-        positions = (work.context_lengths - 1).to(torch.int64).cpu()
-        desc = torch.stack([torch.arange(work.rows), depths.to(torch.int64), positions], 1).to(device)
-        fin_ms = graph_time_ms(
-            [lambda: kv_finalize(work.key_cache, work.value_cache, desc, table_dev, planes)] * 32)
-        slot = work.key_cache.shape[3] * work.key_cache.shape[4] * work.key_cache.element_size()
-        fin_bytes = int((planes - 1 - depths).sum()) * layers * slot * 2 * 2
-        extras["finalize_64_tokens_24_layers"] = {
-            "gbs": round(fin_bytes / (fin_ms * 1e-3) / 1e9, 2), "us": round(fin_ms * 1e3, 2),
-            "bytes": fin_bytes}
+        extras.update(pool_movers(work))
         result["cpu_baseline"] = cpu_baseline(work, args.cpu_seconds)
         del work, kviews, vviews
         torch.cuda.empty_cache()
