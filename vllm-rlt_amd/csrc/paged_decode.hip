@@ -51,6 +51,9 @@ namespace {
 #define VRH_DECODE_PREFETCH 0
 #endif
 
+#ifndef VRH_DECODE_LPT
+#define VRH_DECODE_LPT 1
+#endif
 #ifndef VRH_DECODE_MAX_HPW
 #define VRH_DECODE_MAX_HPW 8  // grouped-query heads one wave may serve
 #endif
@@ -84,6 +87,7 @@ struct DecodeArgs {
   int64_t v_block, v_token, v_head;
   int64_t table_stride;
   int64_t row_base;
+  int64_t rows;      // rows of the whole call (the launch may cover a chunk)
   // Packed-prefill expansion (null for decode): row r is query i of sequence
   // s with cu_q[s] <= r < cu_q[s+1]; it reads table row s with causal length
   // lengths[s] - q_len(s) + i + 1.
@@ -156,6 +160,17 @@ __device__ __forceinline__ int row_length(int64_t row, const DecodeArgs& a, int6
   *table_row = seq;
   *query_row = a.cu_q[seq] + i;
   return clamp_length(a.lengths[seq] - q_len + i + 1, a);
+}
+
+// Maximum of an int over the wave: DPP within rows of 16 lanes, then the 4
+// row results through scalar reads (no LDS traffic).
+__device__ __forceinline__ int wave_max_i(int x) {
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, kDppQuadXor1, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, kDppQuadXor2, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, kDppRowHalfMirror, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, kDppRowMirror, 0xF, 0xF, false));
+  return max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+             max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
 }
 
 // The work of one row and HPW consecutive q heads of one kv head (the
@@ -353,7 +368,44 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
 template <typename T, int VEC, int LPT, int HPW>
 __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   const int head = blockIdx.y * HPW;
-  const int64_t row = a.row_base + blockIdx.z;
+  int64_t row = a.row_base + blockIdx.z;
+#if VRH_DECODE_LPT
+  // Longest splits first: within each group of 64 consecutive rows, grid
+  // row slot z takes the row of rank z by split length (pages per split,
+  // descending; ties keep row order, so rows whose splits are equally long,
+  // e.g. neighbours sharing a prefix, stay together). Workgroups are
+  // dispatched in slot order, so the long splits start first and the drain
+  // at the end of the launch is made of short ones. Every wave of the group
+  // ranks the same 64 rows (one coalesced load; the compare loop only runs
+  // when the split lengths differ), so no extra launch is needed.
+  if (a.cu_q == nullptr) {
+    const int lane = threadIdx.x & 63;
+    const int64_t g0 = row - (blockIdx.z & 63);
+    const int64_t mine = g0 + lane;
+    int key = -1;
+    if (mine < a.rows) {
+      const int n = clamp_length(a.lengths[mine], a);
+      key = n > 0 ? partition(n, a).bps : 0;
+    }
+    const int slot = (int)(blockIdx.z & 63);
+    // Rank only when the group's split lengths differ by 2x or more: only then
+    // does the order shorten the drain (and rows of equal split length, such
+    // as rows sharing a prefix, keep their dispatch neighbourhood).
+    const int kmax = wave_max_i(key);
+    const int kmin = -wave_max_i(key >= 0 ? -key : INT32_MIN + 1);
+    if (kmax >= 2 * kmin || (kmin < 0 && kmax >= 0)) {
+      int rank = 0;
+#pragma unroll
+      for (int j = 0; j < 64; ++j) {
+        const int other = __builtin_amdgcn_readlane(key, j);
+        rank += (other > key) || (other == key && j < lane);
+      }
+      const uint64_t hit = __ballot(rank == slot && key >= 0);
+      if (hit == 0) return;  // slot past the last row of a partial group
+      row = g0 + __builtin_ffsll((long long)hit) - 1;
+    }
+  }
+#endif
   // Workgroup L = x + gx * (head + heads * row) runs on XCD L % 8. Rows need
   // different split counts, so with split = x the low split indices (present
   // in every row) would pile onto the same XCDs; rotating the split index by
@@ -557,6 +609,7 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
   a.v = value_cache;
   a.tables = block_tables;
   a.lengths = context_lengths;
+  a.rows = rows;
   a.part_ml = nullptr;
   a.part_acc = nullptr;
   if (workspace != nullptr) {
@@ -604,9 +657,12 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
   // function of shapes only (graph capture), never of device lengths.
   const int max_pages = std::max(1, table_width);
   const int gx = std::max(1, std::min(kMaxSplits, ceil_div(max_pages, a.min_bps)));
-  for (int64_t first = 0; first < rows; first += 65535) {
+  // Rows per launch: the grid's z limit rounded down to whole 64-row groups
+  // (the longest-first ranking works on aligned groups of 64 rows).
+  constexpr int64_t kRowsPerLaunch = 65535 / 64 * 64;
+  for (int64_t first = 0; first < rows; first += kRowsPerLaunch) {
     a.row_base = first;
-    const unsigned count = (unsigned)std::min<int64_t>(rows - first, 65535);
+    const unsigned count = (unsigned)std::min<int64_t>(rows - first, kRowsPerLaunch);
     bool ok = false;
     dim3 grid((unsigned)gx, (unsigned)(q_heads / hpw), count);
     switch (dtype) {
