@@ -29,6 +29,7 @@
 //    a merge kernel combines them in split order (log-sum-exp). Single-split
 //    rows write the output directly.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -62,6 +63,11 @@ namespace {
 #endif
 constexpr int kMaxSplits = VRH_MAX_SPLITS;
 constexpr int kSplitTokens = VRH_SPLIT_TOKENS;  // minimum tokens per split (whole pages)
+#ifndef VRH_DECODE_DOT2
+#define VRH_DECODE_DOT2 1
+#endif
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
 constexpr int kU = VRH_DECODE_U;                // wave loads per chunk (K and V each)
 
 template <typename T, int VEC>
@@ -209,9 +215,22 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
   }
   const Partition P = partition(n, a);
   if (split0 >= P.nsplit) return;
+  // bf16 with 8-element vectors: the q.k product runs on packed bf16 pairs
+  // (v_dot2 with fp32 accumulation, products exact in fp32) against the
+  // unscaled q; the scale is applied to the reduced score.
+  constexpr bool kDot2 = VRH_DECODE_DOT2 && std::is_same<T, bf16_t>::value && VEC == 8;
+  uint32_t qp2[HPW][VEC / 2];
   float qf[HPW][VEC];
 #pragma unroll
   for (int h = 0; h < HPW; ++h) {
+    if constexpr (kDot2) {
+      const T* qp = reinterpret_cast<const T*>(a.q) + qrow * a.q_row +
+                    (int64_t)(head0 + h) * a.q_head + dg * VEC;
+      const raw_t r = dvalid ? load_raw<T, VEC>(qp) : raw_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < VEC / 2; ++i) qp2[h][i] = r[i];
+      continue;
+    }
     const T* qp = reinterpret_cast<const T*>(a.q) + qrow * a.q_row +
                   (int64_t)(head0 + h) * a.q_head + dg * VEC;
     if (dvalid) {
@@ -284,14 +303,23 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           float kf[VEC];
-          unpack<T, VEC>(kr[u], kf);
+          if constexpr (!kDot2) unpack<T, VEC>(kr[u], kf);
           const bool visible = p0 + u * TPL + tg < s_te;
 #pragma unroll
           for (int h = 0; h < HPW; ++h) {
             float d = 0.f;
+            if constexpr (kDot2) {
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) d = fmaf(qf[h][i], kf[i], d);
-            d = group_sum<LPT>(d);
+              for (int i = 0; i < VEC / 2; ++i)
+                d = __builtin_amdgcn_fdot2_f32_bf16(
+                    __builtin_bit_cast(bf16x2_t, qp2[h][i]),
+                    __builtin_bit_cast(bf16x2_t, (uint32_t)kr[u][i]), d, false);
+              d = group_sum<LPT>(d) * a.scale_log2;
+            } else {
+#pragma unroll
+              for (int i = 0; i < VEC; ++i) d = fmaf(qf[h][i], kf[i], d);
+              d = group_sum<LPT>(d);
+            }
             sc[h][u] = visible ? d : -INFINITY;
             mx[h] = fmaxf(mx[h], sc[h][u]);
           }
