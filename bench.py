@@ -641,6 +641,7 @@ def main():
     import torch
 
     from vllm_rlt import workloads
+    from vllm_rlt.kernels._extension import load_extension
     from vllm_rlt.kernels._hip import library
     from vllm_rlt.kernels.hip_attention import (
         kv_append,
@@ -742,6 +743,25 @@ def main():
         # ctypes boundary (host argument marshalling included), for comparison
         # with the graph-replayed step above.
         eager_ms = event_time_ms(eager_step, 20)
+        # The same step through the registered torch op (vllm_rlt._C), and the
+        # host time per call of each boundary (submission only: the GPU runs
+        # behind, so the host loop measures argument checks and marshalling).
+        load_extension()
+        decode_op = torch.ops.vllm_rlt_hip.paged_attention
+
+        def eager_op_step():
+            for layer in range(layers):
+                decode_op(q, kviews[layer], vviews[layer], tables, lengths, 0)
+
+        eager_op_ms = event_time_ms(eager_op_step, 20)
+        host_us = {}
+        for name, fn in (("ctypes", eager_step), ("torch_op", eager_op_step)):
+            torch.cuda.synchronize()
+            t_host = time.perf_counter()
+            for _ in range(4):
+                fn()
+            host_us[name] = round((time.perf_counter() - t_host) * 1e6 / (4 * layers), 2)
+            torch.cuda.synchronize()
         # 24-layer batched append of the step's 64 tokens (one launch), over
         # 48 disjoint input / destination sets (1.2 GB in all).
         fns, append_layers_bytes, keep = rotating_append_layers(work)
@@ -755,6 +775,8 @@ def main():
         extras = {
             "decode_step_eager_ms": round(eager_ms, 4),
             "decode_step_eager_gbs": round(step_bytes / (eager_ms * 1e-3) / 1e9, 2),
+            "decode_step_eager_torch_op_ms": round(eager_op_ms, 4),
+            "decode_call_host_us": host_us,
             "append_24_layers": {
                 "gbs": round(append_layers_bytes / (append_layers_ms * 1e-3) / 1e9, 2),
                 "us": round(append_layers_ms * 1e3, 2), "bytes": append_layers_bytes,
