@@ -509,23 +509,24 @@ def decode_config5_leg(device, calls=6):
     return out
 
 
-def decode_gqa_leg(device, calls=8):
-    """Grouped-query decode: config 2's 64 rows and context range with 32 q
-    heads over 8 kv heads (head_dim 128, bf16). Algorithmic bytes count each
-    K/V byte once per row (what one wave per kv head group reads)."""
+def decode_gqa_leg(device, calls=8, q_heads=32, kv_heads=8):
+    """Grouped-query decode: config 2's 64 rows and context range with q_heads
+    q heads over kv_heads kv heads (head_dim 128, bf16). Algorithmic bytes
+    count each K/V byte once per row (what one wave per kv head reads). Groups
+    of 4 run on the VALU kernel, groups of 8 on the MFMA kernel."""
     import torch
 
     from vllm_rlt import workloads
     from vllm_rlt.kernels.hip_attention import paged_attention
 
-    w = workloads.gqa_decode(device=device)
+    w = workloads.gqa_decode(device=device, q_heads=q_heads, kv_heads=kv_heads)
     kc, vc = w.key_cache[:, 0], w.value_cache[:, 0]
     call = lambda: paged_attention(w.q, kc, vc, w.block_tables, w.context_lengths)  # noqa: E731
     ms = graph_time_ms([call] * calls, replays=4)
     nbytes = w.decode_bytes()
     out = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 2), "us": round(ms * 1e3, 2),
            "pct_of_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
-           "bytes_per_call": nbytes, "rows": w.rows, "q_heads": 32, "kv_heads": 8}
+           "bytes_per_call": nbytes, "rows": w.rows, "q_heads": q_heads, "kv_heads": kv_heads}
     del w, kc, vc
     torch.cuda.empty_cache()
     return out
@@ -621,6 +622,8 @@ def single_leg(name, repeats):
         print(json.dumps({"leg": name, **out}), flush=True)
     elif name == "decode_gqa":
         print(json.dumps({"leg": name, **decode_gqa_leg(device, calls=repeats)}), flush=True)
+        print(json.dumps({"leg": name, **decode_gqa_leg(device, calls=repeats, q_heads=64)}),
+              flush=True)
     elif name == "decode_config5":
         print(json.dumps({"leg": name, **decode_config5_leg(device, calls=repeats)}),
               flush=True)
@@ -806,6 +809,7 @@ def main():
               "192 GiB config-5 pool", file=sys.stderr, flush=True)
         extras["decode_config5_long_context"] = decode_config5_leg(device)
         extras["decode_gqa_32q_8kv"] = decode_gqa_leg(device)
+        extras["decode_gqa_64q_8kv"] = decode_gqa_leg(device, q_heads=64)
         pw = workloads.config4(device=device)
         kc, vc = pw.key_cache[:, 0], pw.value_cache[:, 0]
         fns, append_bytes, keep, append_rows = rotating_append_config4(pw)
