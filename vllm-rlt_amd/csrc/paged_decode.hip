@@ -5,11 +5,12 @@
 // own block table, GQA head h reads kv head h / G, scores scaled by 1/sqrt(D),
 // fp32 softmax, output rounded to the storage dtype, zero rows for length 0.
 //
-// Design (bandwidth-bound; every K/V byte is read once per group of up to 8
-// q heads that share its kv head):
+// Design (bandwidth-bound; every K/V byte is read once per row and kv head
+// for groups of up to 16 q heads):
 //  * One 64-lane wavefront per (split, group of HPW q heads, row): HPW = 8, 4
 //    or 2 grouped-query heads when they divide the group (each loaded K/V
-//    vector serves all of them), else 1. A split is a run of whole
+//    vector serves all of them), else 1. Groups of 8-16 heads, and of 3, 5, 6
+//    or 7, run on the MFMA kernel below instead (one wave per kv head). A split is a run of whole
 //    pages: bps = max(min_bps, ceil(pages / kMaxSplits)) pages (at least 128
 //    tokens, at most 16 splits per row), so the partition depends only on
 //    the row's own length -> batch invariance. The split index is rotated
