@@ -80,6 +80,24 @@ def test_noalloc_f32_window_and_gqa(gpu):
         assert torch.equal(got, want)
 
 
+def test_noalloc_grouped_query_mfma_twice(gpu):
+    """Groups of 8 q heads per kv head (the MFMA decode kernel), bf16: two
+    calls in a row, the second with fewer rows, against the workspace entry."""
+    from vllm_rlt.kernels._hip import library
+    from vllm_rlt.kernels.hip_attention import paged_attention, paged_attention_noalloc
+
+    library()
+    for rows, max_len, seed in ((24, 3000, 6), (5, 400, 7)):
+        print(f"noalloc: bf16 32 q heads over 4 kv heads, {rows} rows up to {max_len} tokens",
+              flush=True)
+        q, k, v, tables, lengths = _inputs(rows, max_len, seed=seed, heads=4)
+        q = q.repeat_interleave(8, dim=1).contiguous()
+        want = paged_attention(q, k, v, tables, lengths)
+        got = paged_attention_noalloc(q, k, v, tables, lengths)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+
+
 def test_noalloc_rejects_sizes_beyond_the_scratch(gpu):
     from vllm_rlt.kernels._hip import library
 
