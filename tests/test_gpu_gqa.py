@@ -83,3 +83,28 @@ def test_gqa_decode_packed_prefill_decode_rows(gpu):
     cu = torch.tensor([0, 1, 2, 3, 4], dtype=torch.int32, device=gpu)
     actual = paged_prefill_attention(q, k, v, tables, context, cu, max(q_lens))
     assert_close(actual, oracle_decode(q, k, v, tables, context), torch.bfloat16)
+
+
+def test_gqa_decode_graph_replays(gpu):
+    """The MFMA path captured in a HIP graph: three replays, with eager work
+    and synchronisations between them, each equal to the eager result."""
+    from vllm_rlt.kernels.hip_attention import paged_attention
+
+    q, k, v, tables, context = random_paged(LENGTHS, 32, 2, 128, torch.bfloat16, gpu, seed=21)
+    eager = paged_attention(q, k, v, tables, context)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        paged_attention(q, k, v, tables, context)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = paged_attention(q, k, v, tables, context)
+    for _ in range(3):
+        captured.fill_(float("nan"))
+        paged_attention(q[:3], k, v, tables[:3], context[:3])  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager)
