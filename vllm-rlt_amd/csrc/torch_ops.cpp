@@ -255,10 +255,10 @@ void kv_copy_blocks(const at::Tensor& kc, const at::Tensor& vc, const at::Tensor
   check_int("src_blocks", src_in, at::kLong, 1, kc.device());
   check_int("dst_blocks", dst_in, at::kLong, 1, kc.device());
   TORCH_CHECK(src_in.size(0) == dst_in.size(0), "src_blocks and dst_blocks must have equal lengths");
-  const at::Tensor block = kc[0];
-  TORCH_CHECK(block.is_contiguous(), "each pool block must be contiguous");
   const int64_t n = src_in.size(0);
   if (n == 0) return;
+  const at::Tensor block = kc[0];
+  TORCH_CHECK(block.is_contiguous(), "each pool block must be contiguous");
   const c10::DeviceGuard guard(kc.device());
   const at::Tensor src = src_in.contiguous(), dst = dst_in.contiguous();
   const int64_t es = kc.element_size();
