@@ -51,7 +51,7 @@ constexpr int kWQ = 32;                    // queries per wave
 constexpr int kBM = kWQ * kWaves;          // queries per workgroup
 constexpr int kSB = 32;                    // keys per sub-block (one pipeline step)
 #ifndef VRH_PREFILL_STAGES
-#define VRH_PREFILL_STAGES 3
+#define VRH_PREFILL_STAGES 4
 #endif
 constexpr int kStages = VRH_PREFILL_STAGES;  // LDS half-stages: one sub-block each
 static_assert(kStages >= 3 && kStages <= 4, "stages");
@@ -140,6 +140,29 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
   const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (v4s __attribute__((address_space(3)))*)(const_cast<uint16_t*>(p)));
   return __builtin_bit_cast(u32x2, r);
+}
+
+#ifndef VRH_PREFILL_DMA
+#define VRH_PREFILL_DMA 1
+#endif
+
+// LDS byte offset of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// One 16-byte-per-lane load from global memory into LDS at m0 + 16 * lane.
+// The s_nop is the wait state an LDS-direct load needs after an M0 write
+// (the compiler inserts it for the instructions it knows, not inside asm).
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t m0) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt not waited on).
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 16, "vmcnt");
+  __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0xF << 8));
 }
 
 #ifndef VRH_PREFILL_SAME_KV32
@@ -265,7 +288,9 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
   const T* lane_k = kg + (int64_t)lane_row * a.k_token + lane_dof;
   const T* lane_v = vg + (int64_t)lane_row * a.v_token + lane_dof;
   struct Regs { u32x4 k[NI]; u32x4 v[NI]; };
-  auto gather = [&](int j, Regs& R) {
+  // Addresses of sub-block j's K and V vectors for this wave's staging
+  // instructions r = 0 .. NI - 1, handed to `sink(r, k_ptr, v_ptr)`.
+  auto gather_to = [&](int j, auto&& sink) {
     const int k0 = j * kSB;
     {
       const int last_page = page_of(min(k0 + kSB, end) - 1);
@@ -284,8 +309,7 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
         const uint32_t row_off = pb & (a.block_size - 1);
         const uint64_t off = (uint64_t)page * (uint32_t)a.k_block +
                              (uint64_t)row_off * (uint32_t)a.k_token;
-        R.k[r] = *reinterpret_cast<const u32x4*>(lane_k + off);
-        R.v[r] = *reinterpret_cast<const u32x4*>(lane_v + off);
+        sink(r, lane_k + off, lane_v + off);
       }
       return;
     }
@@ -298,8 +322,8 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
         const int pg = pb >> a.bs_shift;
         const int64_t page = __builtin_amdgcn_readfirstlane(tbl_lds[pg - tbl_base]);
         const int64_t row_off = pb & (a.block_size - 1);
-        R.k[r] = *reinterpret_cast<const u32x4*>(lane_k + (page * a.k_block + row_off * a.k_token));
-        R.v[r] = *reinterpret_cast<const u32x4*>(lane_v + (page * a.v_block + row_off * a.v_token));
+        sink(r, lane_k + (page * a.k_block + row_off * a.k_token),
+             lane_v + (page * a.v_block + row_off * a.v_token));
       }
       return;
     }
@@ -314,9 +338,29 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
       const int pg = page_of(pos);
       const int64_t page = tbl_lds[pg - tbl_base];
       const int64_t toks = pos - pg * a.block_size - (kPow2 ? lane_row : 0);
-      R.k[r] = *reinterpret_cast<const u32x4*>((kPow2 ? lane_k : kg) + page * a.k_block + toks * a.k_token + dof);
-      R.v[r] = *reinterpret_cast<const u32x4*>((kPow2 ? lane_v : vg) + page * a.v_block + toks * a.v_token + dof);
+      sink(r, (kPow2 ? lane_k : kg) + page * a.k_block + toks * a.k_token + dof,
+           (kPow2 ? lane_v : vg) + page * a.v_block + toks * a.v_token + dof);
     }
+  };
+  auto gather = [&](int j, Regs& R) {
+    gather_to(j, [&](int r, const T* kp, const T* vp) {
+      R.k[r] = *reinterpret_cast<const u32x4*>(kp);
+      R.v[r] = *reinterpret_cast<const u32x4*>(vp);
+    });
+  };
+  // Sub-block j straight into LDS stage `stage` (global_load_lds_dwordx4: lane
+  // l's 16 bytes land at M0 + 16 l, the same slots `put` writes). The loads
+  // are issued as inline assembly so that the compiler neither waits for them
+  // nor orders LDS reads behind them; the pipeline waits explicitly
+  // (vm_wait below) before the barrier that publishes a stage.
+  auto dma = [&](int j, auto stage_c) {
+    constexpr int stage = decltype(stage_c)::value;
+    const uint32_t kl = lds_offset(ks[stage]) + 1024 * wave;
+    const uint32_t vl = lds_offset(vs[stage]) + 1024 * wave;
+    gather_to(j, [&](int r, const T* kp, const T* vp) {
+      lds_dma16(kp, __builtin_amdgcn_readfirstlane(kl + 1024 * kWaves * r));
+      lds_dma16(vp, __builtin_amdgcn_readfirstlane(vl + 1024 * kWaves * r));
+    });
   };
   auto put = [&](auto stage_c, const Regs& R) {
     constexpr int stage = decltype(stage_c)::value;
@@ -470,12 +514,30 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
   using H2 = std::integral_constant<int, 2>;
   using H3 = std::integral_constant<int, 3>;
   f32x16 st = f32x16{};
+  // LDS-direct staging (sub-block j + 3 loaded into LDS at step j: two steps
+  // of load latency) where every wave issues the same number of staging
+  // loads per sub-block, so that one vmcnt bound fits every wave; otherwise
+  // staging through registers (sub-block j + 3 gathered at step j, stored at
+  // step j + 1).
+  constexpr bool kDma = VRH_PREFILL_DMA && kStages == 4 && SB_INST % kWaves == 0;
+  constexpr int kDmaPerStep = 2 * NI;  // K and V loads per wave per sub-block
   Regs R;
   if (nsub > 0) {
-    gather(0, R);
-    put(H0{}, R);
-    if (nsub > 1) { gather(1, R); put(H1{}, R); }
-    if (nsub > 2) gather(2, R);
+    if constexpr (kDma) {
+      dma(0, H0{});
+      if (nsub > 1) dma(1, H1{});
+      if (nsub > 2) {
+        dma(2, H2{});
+        vm_wait<kDmaPerStep>();  // sub-blocks 0 and 1 have landed
+      } else {
+        vm_wait<0>();
+      }
+    } else {
+      gather(0, R);
+      put(H0{}, R);
+      if (nsub > 1) { gather(1, R); put(H1{}, R); }
+      if (nsub > 2) gather(2, R);
+    }
     __syncthreads();
     if (nsub_w > 0) {
       u32x4 kop[DC];
@@ -487,9 +549,20 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
       constexpr int h = decltype(hc)::value;
       using Hn = std::integral_constant<int, (h + 1) % kStages>;
       using Hp = std::integral_constant<int, (h + 2) % kStages>;
-      __syncthreads();
-      if (j + 2 < nsub) put(Hp{}, R);
-      if (j + 3 < nsub) gather(j + 3, R);
+      if constexpr (kDma) {
+        // Sub-block j + 1 (read by this step) must have landed; only the
+        // loads of j + 2 (issued one step ago) may still be in flight. The
+        // barrier then publishes it and frees the stage of j - 1 for j + 3.
+        using Hd = std::integral_constant<int, (h + 3) % kStages>;
+        if (j + 2 < nsub) vm_wait<kDmaPerStep>();
+        else vm_wait<0>();
+        __syncthreads();
+        if (j + 3 < nsub) dma(j + 3, Hd{});
+      } else {
+        __syncthreads();
+        if (j + 2 < nsub) put(Hp{}, R);
+        if (j + 3 < nsub) gather(j + 3, R);
+      }
       if (j >= nsub_w) return;
       u32x4 pop[2];
       u32x4 vop[DB][2];
