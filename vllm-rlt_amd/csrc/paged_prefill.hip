@@ -8,9 +8,10 @@
 //
 // MFMA path (bf16/f16, head_dim a multiple of 32 up to 128):
 //  * Workgroup = 4 waves = 128 query rows of one (sequence, q head); each wave
-//    owns 32 queries. K/V arrive in 32-key sub-blocks staged through
-//    registers into LDS (three stages) and shared by the 4 waves; one
-//    barrier per sub-block.
+//    owns 32 queries. K/V arrive in 32-key sub-blocks staged into LDS (four
+//    stages; loaded straight into LDS three sub-blocks ahead, or through
+//    registers where the waves' staging loads do not divide evenly) and
+//    shared by the 4 waves; one barrier per sub-block.
 //  * Each wave software-pipelines the sub-blocks: the QK^T MFMAs of sub-block
 //    j + 1 are interleaved with the softmax VALU work of sub-block j.
 //  * S^T = K Q^T with v_mfma_f32_32x32x16_{bf16,f16}: A = K rows from LDS
@@ -498,11 +499,13 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
 
   // Pipeline over 32-key sub-blocks, kStages (3 or 4) LDS stages, sub-block
   // j in stage j % kStages. Step j:
-  //   barrier (sub-block j + 1, stored at step j - 1, is visible; every wave
-  //   has finished step j - 1, the last reader of sub-block j - 1);
-  //   store the registers holding sub-block j + 2 into stage (j + 2) %
-  //   kStages (which held sub-block j - 1 or j - 2), then gather sub-block
-  //   j + 3 into the same registers (one step of latency to land);
+  //   barrier (sub-block j + 1 is in LDS and visible; every wave has
+  //   finished step j - 1, the last reader of sub-block j - 1);
+  //   LDS-direct: load sub-block j + 3 into the stage of j - 1 (two steps of
+  //   latency to land). Register staging: store the registers holding
+  //   sub-block j + 2 into stage (j + 2) % kStages (which held sub-block
+  //   j - 1 or j - 2), then gather sub-block j + 3 into the same registers
+  //   (one step of latency);
   //   S1: every LDS operand read (K of j + 1, V of j), then the QK^T MFMAs of
   //       j + 1 interleaved with the probability VALU work of j;
   //   S2: PV of sub-block j (MFMA) interleaved with the mask / row max of
