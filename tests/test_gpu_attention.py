@@ -231,7 +231,7 @@ def test_packed_prefill_matches_per_query_oracle(gpu, dtype, head_dim, heads, kv
     assert_close(actual, oracle_prefill(q, k, v, tables, lengths, cu), dtype)
 
 
-@pytest.mark.parametrize("block", [2, 5, 8, 32, 64])
+@pytest.mark.parametrize("block", [2, 4, 5, 8, 16, 32, 64])
 @pytest.mark.parametrize("dtype,head_dim,heads,kv_heads", [(torch.bfloat16, 128, 4, 4),
                                                           (torch.float16, 64, 4, 2)])
 def test_packed_prefill_block_sizes_and_long_tables(gpu, block, dtype, head_dim, heads, kv_heads):

@@ -46,7 +46,10 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
 namespace vrh {
 namespace {
 
-constexpr int kWaves = 4;                  // waves per workgroup
+#ifndef VRH_PREFILL_WAVES
+#define VRH_PREFILL_WAVES 4
+#endif
+constexpr int kWaves = VRH_PREFILL_WAVES;  // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kWQ = 32;                    // queries per wave
 constexpr int kBM = kWQ * kWaves;          // queries per workgroup
@@ -170,15 +173,17 @@ __device__ __forceinline__ void vm_wait() {
 #define VRH_PREFILL_SAME_KV32 1
 #endif
 #ifndef VRH_PREFILL_WG_PER_CU
-#define VRH_PREFILL_WG_PER_CU 2
+#define VRH_PREFILL_WG_PER_CU (VRH_PREFILL_WAVES == 8 ? 1 : 2)
 #endif
+// Two waves per SIMD: two 4-wave workgroups or one 8-wave workgroup per CU.
+constexpr int kWavesPerEu = VRH_PREFILL_WG_PER_CU * VRH_PREFILL_WAVES / 4;
 
 // Page addressing modes: kDiv (any block size), kShift (power of two).
 enum PageMode { kDiv = 0, kShift = 1 };
 
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU)
-__attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU))) void paged_prefill_kernel(PrefillArgs a) {
+__attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefill_kernel(PrefillArgs a) {
   constexpr int DC = D / 16;                   // 16-wide d chunks (QK^T k-steps)
   constexpr int DB = D / 32;                   // 32-row d blocks of O^T
   constexpr int KCH = D / 8;                   // 16-byte chunks per key row
@@ -278,16 +283,23 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
   // v / KCH. Branch-free: keys past `end` re-read key end - 1 (real data);
   // the softmax masks them.
   // With KCH a power of two a lane keeps its chunk and its row advances by
-  // S = 256 / KCH per instruction, so the swizzled chunk offset and the row
-  // term of the address are per-lane constants. When the block size is a
-  // multiple of S, the S rows of one instruction share a page: a full
-  // sub-block then needs one (wave-uniform) page-id read per instruction.
+  // S = 64 * kWaves / KCH per instruction, so the swizzled chunk offset (the
+  // swizzle depends on row % 16, and S is a multiple of 16) is a per-lane
+  // constant. One instruction covers the IR = 64 / KCH consecutive rows
+  // starting at row k0 + IR * inst; when the block size is a multiple of IR
+  // they share a page, so a full sub-block needs one (wave-uniform) page-id
+  // read per instruction and the lane adds its row within the instruction.
   constexpr bool kPow2 = (KCH & (KCH - 1)) == 0;
-  constexpr int S = 256 / KCH;
+  constexpr int S = 64 * kWaves / KCH;
+  constexpr int IR = 64 / KCH;
+  static_assert(!kPow2 || S % 16 == 0, "swizzle period");
   const int lane_row = (64 * wave + lane) / KCH;
   const int lane_dof = kPow2 ? (((64 * wave + lane) % KCH) ^ L::swizzle(lane_row)) * 8 : 0;
+  const int lane_in = lane / KCH;  // row within one instruction's IR rows
   const T* lane_k = kg + (int64_t)lane_row * a.k_token + lane_dof;
   const T* lane_v = vg + (int64_t)lane_row * a.v_token + lane_dof;
+  const T* lane_k1 = kg + (int64_t)lane_in * a.k_token + lane_dof;
+  const T* lane_v1 = vg + (int64_t)lane_in * a.v_token + lane_dof;
   struct Regs { u32x4 k[NI]; u32x4 v[NI]; };
   // Addresses of sub-block j's K and V vectors for this wave's staging
   // instructions r = 0 .. NI - 1, handed to `sink(r, k_ptr, v_ptr)`.
@@ -305,12 +317,12 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
       for (int r = 0; r < NI; ++r) {
         const int inst = wave + kWaves * r;
         if (pad(inst)) continue;
-        const int pb = k0 + r * S;
+        const int pb = k0 + IR * inst;  // first row of this instruction
         const uint32_t page = __builtin_amdgcn_readfirstlane(tbl_lds[(pb >> a.bs_shift) - tbl_base]);
-        const uint32_t row_off = pb & (a.block_size - 1);
+        const uint32_t row_off = __builtin_amdgcn_readfirstlane(pb & (a.block_size - 1));
         const uint64_t off = (uint64_t)page * (uint32_t)a.k_block +
                              (uint64_t)row_off * (uint32_t)a.k_token;
-        sink(r, lane_k + off, lane_v + off);
+        sink(r, lane_k1 + off, lane_v1 + off);
       }
       return;
     }
@@ -319,12 +331,12 @@ __attribute__((amdgpu_waves_per_eu(VRH_PREFILL_WG_PER_CU, VRH_PREFILL_WG_PER_CU)
       for (int r = 0; r < NI; ++r) {
         const int inst = wave + kWaves * r;
         if (pad(inst)) continue;
-        const int pb = k0 + r * S;
+        const int pb = k0 + IR * inst;  // first row of this instruction
         const int pg = pb >> a.bs_shift;
         const int64_t page = __builtin_amdgcn_readfirstlane(tbl_lds[pg - tbl_base]);
-        const int64_t row_off = pb & (a.block_size - 1);
-        sink(r, lane_k + (page * a.k_block + row_off * a.k_token),
-             lane_v + (page * a.v_block + row_off * a.v_token));
+        const int64_t row_off = __builtin_amdgcn_readfirstlane(pb & (a.block_size - 1));
+        sink(r, lane_k1 + (page * a.k_block + row_off * a.k_token),
+             lane_v1 + (page * a.v_block + row_off * a.v_token));
       }
       return;
     }
@@ -775,10 +787,11 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   a.table_width = table_width;
   a.skip_q = route_decode ? kDecodeQ : 0;
   {
-    // Rows per DMA instruction step in the kernel: 256 / (head_dim / 8).
+    // Rows one staging instruction covers: 64 lanes of 16 bytes over rows of
+    // head_dim / 8 chunks; the fast addressing needs them on one page.
     const int chunks = head_dim / 8;
     const bool pow2_chunks = (chunks & (chunks - 1)) == 0;
-    a.uniform_pages = pow2_chunks && a.bs_shift >= 0 && block_size % (256 / chunks) == 0;
+    a.uniform_pages = pow2_chunks && a.bs_shift >= 0 && block_size % (64 / chunks) == 0;
   }
   a.same_kv32 = VRH_PREFILL_SAME_KV32 && k_block_stride == v_block_stride &&
                 k_token_stride == v_token_stride && k_block_stride >= 0 &&
