@@ -157,6 +157,29 @@ __device__ __forceinline__ typename Vec<T, VEC>::raw_t pack(const float (&in)[VE
   return v.raw;
 }
 
+// ------------------------------------------------------- LDS-direct loads
+// LDS byte offset of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// One 16-byte-per-lane load from global memory into LDS at m0 + 16 * lane
+// (global_load_lds_dwordx4). Issued as inline assembly so that the compiler
+// neither waits for it nor orders LDS reads behind it: the caller bounds it
+// with vm_wait before reading the LDS it fills. The s_nop is the wait state an
+// LDS-direct load needs after an M0 write (the compiler inserts it for the
+// instructions it knows, not inside asm).
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t m0) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt not waited on).
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 16, "vmcnt");
+  __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0xF << 8));
+}
+
 // ------------------------------------------------------------ wave reductions
 // DPP control words (GCN/CDNA "row" = 16 lanes).
 constexpr int kDppQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]

@@ -472,6 +472,9 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
 #ifndef VRH_DECODE_MFMA_GQA
 #define VRH_DECODE_MFMA_GQA 1
 #endif
+#ifndef VRH_MFMA_ALL_GROUPS
+#define VRH_MFMA_ALL_GROUPS 8  // groups this large always take the MFMA kernel
+#endif
 constexpr int kMfmaMinGroup = 3;    // smaller groups use the VALU kernel
 constexpr int kMfmaHeads = 16;      // q heads per tile (MFMA columns)
 constexpr int kMfmaChunk = 32;      // tokens per PV step
@@ -558,22 +561,30 @@ __device__ __forceinline__ void decode_work_mfma(const DecodeArgs& a, int64_t ro
     }
   }
   const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)kvh * a.k_head + 8 * grp;
-  const int v_chunk = lane % KCH;
+  // V staging: instruction r loads token rows RPI r .. + RPI - 1 straight
+  // into LDS (lane l's 16 bytes land at row RPI r + l / KCH, slot l % KCH), so
+  // the lane fetches the chunk stored at that slot: slot ^ swizzle(row). The
+  // swizzle depends on row % 16 and RPI * r repeats it every 16 / RPI
+  // instructions.
   const int v_row = lane / KCH;
-  const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)kvh * a.v_head + 8 * v_chunk;
+  constexpr int SWP = 16 / RPI < NV ? 16 / RPI : NV;  // distinct swizzles
+  const T* vbase[SWP];
+#pragma unroll
+  for (int r = 0; r < SWP; ++r) {
+    const int row = v_row + RPI * r;
+    vbase[r] = reinterpret_cast<const T*>(a.v) + (int64_t)kvh * a.v_head +
+               (vt_at<D>(row, 8 * (lane % KCH)) - row * D);
+  }
+  // The chunk index the swizzle yields is the element offset's chunk part:
+  // vt_at(row, 8 s) - row D is 8 (s ^ swizzle(row)), an involution, so the
+  // lane's global chunk is the one vt_at maps its slot to.
+  const uint32_t vt_lds = lds_offset(vt);
   const int32_t* table = a.tables + trow * a.table_stride;
-  // LDS element offsets: staging store of row v_row + RPI * r; transposed
-  // reads of tile t, token half h: rows 16h + 4grp + (col >> 2), dims
-  // 16t + 4(col & 3).
-  uint32_t st_off[NV];
+  // Transposed reads of tile t, token half h: rows 16h + 4grp + (col >> 2),
+  // dims 16t + 4(col & 3); half 1 is 16 rows (16 D elements) further.
+  uint32_t tr_off[DT];
 #pragma unroll
-  for (int r = 0; r < NV; ++r) st_off[r] = vt_at<D>(v_row + RPI * r, 8 * v_chunk);
-  uint32_t tr_off[DT][2];
-#pragma unroll
-  for (int t = 0; t < DT; ++t)
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      tr_off[t][h] = vt_at<D>(16 * h + 4 * grp + (col >> 2), 16 * t + 4 * (col & 3));
+  for (int t = 0; t < DT; ++t) tr_off[t] = vt_at<D>(4 * grp + (col >> 2), 16 * t + 4 * (col & 3));
 
   auto page_addr = [&](int pos, int tbl, int seg, int64_t blk_stride, int64_t tok_stride) {
     int page, off;
@@ -614,12 +625,13 @@ __device__ __forceinline__ void decode_work_mfma(const DecodeArgs& a, int64_t ro
           for (int c = 0; c < DC; ++c)
             kop[t][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kp + 32 * c));
         }
-        u32x4_t vraw[NV];
+        // V straight into the LDS tile. The previous chunk's transposed reads
+        // have returned (its PV MFMAs consumed them), so the tile is free.
 #pragma unroll
         for (int r = 0; r < NV; ++r) {
           const int pos = min(p0 + v_row + RPI * r, s_te - 1);
-          const T* vp = vbase + page_addr(pos, tbl, seg, a.v_block, a.v_token);
-          vraw[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(vp));
+          const T* vp = vbase[r % SWP] + page_addr(pos, tbl, seg, a.v_block, a.v_token);
+          lds_dma16(vp, __builtin_amdgcn_readfirstlane(vt_lds + 1024 * r));
         }
         // S tiles and their masked max (tokens p0 + 16t + 4grp + i).
         f32x4_t sc[2];
@@ -629,10 +641,6 @@ __device__ __forceinline__ void decode_work_mfma(const DecodeArgs& a, int64_t ro
 #pragma unroll
           for (int c = 0; c < DC; ++c) sc[t] = Mfma16<T>::run(kop[t][c], qop[c], sc[t]);
         }
-        // The V tile of the previous chunk has been read (in-order LDS within
-        // the wave), so the stores may overwrite it.
-#pragma unroll
-        for (int r = 0; r < NV; ++r) *reinterpret_cast<u32x4_t*>(vt + st_off[r]) = vraw[r];
         const int lim = s_te - p0 - 4 * grp;  // token slot t*16 + i visible when < lim
         float mx = -INFINITY;
 #pragma unroll
@@ -663,10 +671,11 @@ __device__ __forceinline__ void decode_work_mfma(const DecodeArgs& a, int64_t ro
           }
         const u32x4_t pop = u32x4_t{pack2<T>(p[0][0], p[0][1]), pack2<T>(p[0][2], p[0][3]),
                                     pack2<T>(p[1][0], p[1][1]), pack2<T>(p[1][2], p[1][3])};
+        vm_wait<0>();  // the V tile has landed
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-          const u32x2_t lo = lds_tr16(vt + tr_off[t][0]);
-          const u32x2_t hi = lds_tr16(vt + tr_off[t][1]);
+          const u32x2_t lo = lds_tr16(vt + tr_off[t]);
+          const u32x2_t hi = lds_tr16(vt + tr_off[t] + 16 * D);
           acc[t] = Mfma16<T>::run(u32x4_t{lo[0], lo[1], hi[0], hi[1]}, pop, acc[t]);
         }
       }
@@ -950,7 +959,7 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
   const bool mfma_gqa = VRH_DECODE_MFMA_GQA &&
                         (dtype == VRH_DTYPE_BF16 || dtype == VRH_DTYPE_F16) && vec * es == 16 &&
                         (head_dim == 64 || head_dim == 128) && a.group >= kMfmaMinGroup &&
-                        a.group <= kMfmaHeads && (a.group >= 8 || hpw < a.group);
+                        a.group <= kMfmaHeads && (a.group >= VRH_MFMA_ALL_GROUPS || hpw < a.group);
   // Largest split count any row of this table width can need: the grid is a
   // function of shapes only (graph capture), never of device lengths.
   const int max_pages = std::max(1, table_width);

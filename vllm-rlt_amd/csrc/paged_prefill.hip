@@ -150,25 +150,6 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
 #define VRH_PREFILL_DMA 1
 #endif
 
-// LDS byte offset of a __shared__ object.
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// One 16-byte-per-lane load from global memory into LDS at m0 + 16 * lane.
-// The s_nop is the wait state an LDS-direct load needs after an M0 write
-// (the compiler inserts it for the instructions it knows, not inside asm).
-__device__ __forceinline__ void lds_dma16(const void* g, uint32_t m0) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
-}
-
-// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt not waited on).
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  static_assert(N >= 0 && N < 16, "vmcnt");
-  __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0xF << 8));
-}
-
 #ifndef VRH_PREFILL_SAME_KV32
 #define VRH_PREFILL_SAME_KV32 1
 #endif
