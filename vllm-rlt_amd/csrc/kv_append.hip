@@ -10,8 +10,14 @@
 // vectors of one job, so the 4 KiB bf16 K slot of an Ouro token (16 heads x 128)
 // is exactly one 256-thread workgroup of 16-byte vectors. Loads of k/v are
 // ordinary (they were just written by the projection); stores are the only HBM
-// writes of the path and go out as full 64-byte-aligned lines.
+// writes of the path, go out as full 64-byte-aligned lines and are
+// non-temporal: each slot is written once, and its next reader (the attention
+// of the step) reads whole contexts from HBM.
 #include "common.h"
+
+#ifndef VRH_APPEND_NT_STORE
+#define VRH_APPEND_NT_STORE 1
+#endif
 
 namespace vrh {
 namespace {
@@ -59,8 +65,13 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
                                                    lay * a.k_layer + (int64_t)jj * VECB);
   const raw_t vv = *reinterpret_cast<const raw_t*>(a.v + row * a.v_row + h * a.v_head +
                                                    lay * a.v_layer + (int64_t)jj * VECB);
+#if VRH_APPEND_NT_STORE
+  __builtin_nontemporal_store(kv, reinterpret_cast<raw_t*>(a.kc + dst));
+  __builtin_nontemporal_store(vv, reinterpret_cast<raw_t*>(a.vc + dst));
+#else
   *reinterpret_cast<raw_t*>(a.kc + dst) = kv;
   *reinterpret_cast<raw_t*>(a.vc + dst) = vv;
+#endif
 }
 
 }  // namespace
