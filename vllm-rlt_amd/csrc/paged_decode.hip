@@ -22,6 +22,8 @@
 //    re-read the last valid token and are masked).
 //  * The row's page ids for up to 64 pages sit in one VGPR (one per lane) and
 //    are fetched with ds_bpermute, so the page table is read once per split.
+//    Pages shared with a neighbouring row of the batch are read with ordinary
+//    (cache-allocating) loads, the others with non-temporal loads.
 //  * Each token group keeps its own online-softmax state (m, l, acc) in the
 //    log2 domain; groups are merged once per split with cross-lane shuffles,
 //    so the inner loop has no cross-row reductions. QK^T partial sums reduce
@@ -64,6 +66,9 @@ namespace {
 #endif
 constexpr int kMaxSplits = VRH_MAX_SPLITS;
 constexpr int kSplitTokens = VRH_SPLIT_TOKENS;  // minimum tokens per split (whole pages)
+#ifndef VRH_DECODE_SHARED_HINT
+#define VRH_DECODE_SHARED_HINT 1
+#endif
 #ifndef VRH_DECODE_DOT2
 #define VRH_DECODE_DOT2 1
 #endif
@@ -249,148 +254,217 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
   const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)kvh * a.k_head + lane_dim;
   const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)kvh * a.v_head + lane_dim;
   const int32_t* table = a.tables + trow * a.table_stride;
-
-  for (int split = split0; split < P.nsplit; split += step) {
-    const int b0 = P.first + split * P.bps;
-    const int b1 = min(b0 + P.bps, P.first + P.pages);
-    const int tb = max(P.start, b0 * a.block_size);
-    const int te = min(n, b1 * a.block_size);
-
-    float m[HPW], l[HPW];
-    float acc[HPW][VEC];
-#pragma unroll
-    for (int h = 0; h < HPW; ++h) {
-      m[h] = -INFINITY;
-      l[h] = 0.f;
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) acc[h][i] = 0.f;
-    }
-
-    for (int seg = b0; seg < b1; seg += 64) {
-      const int tbl = (seg + lane < b1) ? table[seg + lane] : 0;
-      const int s_tb = max(tb, seg * a.block_size);
-      const int s_te = min(te, (seg + 64) * a.block_size);
-      if (s_tb >= s_te) continue;
-      // Branch-free loads: positions past the end re-read the last valid token
-      // (masked out of the softmax), so a chunk is one straight run of loads.
-      auto issue = [&](int p0, raw_t (&kr)[U], raw_t (&vr)[U]) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int pos = min(p0 + u * TPL + tg, s_te - 1);
-          int page, off;
-          if (a.bs_shift >= 0) {
-            page = pos >> a.bs_shift;
-            off = pos & (a.block_size - 1);
-          } else {
-            page = pos / a.block_size;
-            off = pos - page * a.block_size;
-          }
-          const int64_t blk = shfl_i32(tbl, page - seg);
-          kr[u] = load_kv<T, VEC>(kbase + blk * a.k_block + (int64_t)off * a.k_token);
-          vr[u] = load_kv<T, VEC>(vbase + blk * a.v_block + (int64_t)off * a.v_token);
-        }
-      };
-      raw_t kr[U], vr[U];
-      issue(s_tb, kr, vr);
-      for (int p0 = s_tb; p0 < s_te; p0 += CH) {
-#if VRH_DECODE_PREFETCH
-        raw_t kn[U], vn[U];
-        if (p0 + CH < s_te) issue(p0 + CH, kn, vn);
-#endif
-        float sc[HPW][U];
-        float mx[HPW];
-#pragma unroll
-        for (int h = 0; h < HPW; ++h) mx[h] = m[h];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          float kf[VEC];
-          if constexpr (!kDot2) unpack<T, VEC>(kr[u], kf);
-          const bool visible = p0 + u * TPL + tg < s_te;
-#pragma unroll
-          for (int h = 0; h < HPW; ++h) {
-            float d = 0.f;
-            if constexpr (kDot2) {
-#pragma unroll
-              for (int i = 0; i < VEC / 2; ++i)
-                d = __builtin_amdgcn_fdot2_f32_bf16(
-                    __builtin_bit_cast(bf16x2_t, qp2[h][i]),
-                    __builtin_bit_cast(bf16x2_t, (uint32_t)kr[u][i]), d, false);
-              d = group_sum<LPT>(d) * a.scale_log2;
-            } else {
-#pragma unroll
-              for (int i = 0; i < VEC; ++i) d = fmaf(qf[h][i], kf[i], d);
-              d = group_sum<LPT>(d);
-            }
-            sc[h][u] = visible ? d : -INFINITY;
-            mx[h] = fmaxf(mx[h], sc[h][u]);
-          }
-        }
-        float safe[HPW];
-#pragma unroll
-        for (int h = 0; h < HPW; ++h) {
-          safe[h] = (mx[h] == -INFINITY) ? 0.f : mx[h];
-          const float corr = fast_exp2(m[h] - safe[h]);
-          l[h] *= corr;
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) acc[h][i] *= corr;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          float vf[VEC];
-          unpack<T, VEC>(vr[u], vf);
-#pragma unroll
-          for (int h = 0; h < HPW; ++h) {
-            const float p = fast_exp2(sc[h][u] - safe[h]);
-            l[h] += p;
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) acc[h][i] = fmaf(p, vf[i], acc[h][i]);
-          }
-        }
-#pragma unroll
-        for (int h = 0; h < HPW; ++h) m[h] = mx[h];
-#if VRH_DECODE_PREFETCH
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          kr[u] = kn[u];
-          vr[u] = vn[u];
-        }
-#else
-        if (p0 + CH < s_te) issue(p0 + CH, kr, vr);
-#endif
-      }
-    }
-
-#pragma unroll
-    for (int h = 0; h < HPW; ++h) {
-      // Merge the token groups' states (fixed butterfly order).
-      const float M = cross_group_max<LPT>(m[h]);
-      const float w = (m[h] == -INFINITY) ? 0.f : fast_exp2(m[h] - M);
-      const float L = cross_group_sum<LPT>(l[h] * w);
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) acc[h][i] = cross_group_sum<LPT>(acc[h][i] * w);
-
-      if (P.nsplit == 1) {
-        if (tg == 0 && dvalid) {
-          const float inv = fast_rcp(fmaxf(L, 1e-30f));
-          float o[VEC];
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) o[i] = acc[h][i] * inv;
-          store_raw<T, VEC>(out + h * a.o_head, pack<T, VEC>(o));
-        }
-      } else {
-        const int64_t idx = ((row * a.q_heads + head0 + h) * kMaxSplits) + split;
-        if (lane == 0) {
-          a.part_ml[idx * 2 + 0] = M;
-          a.part_ml[idx * 2 + 1] = L;
-        }
-        if (tg == 0 && dvalid) {
-          float* dst = a.part_acc + idx * a.head_dim + dg * VEC;
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) dst[i] = acc[h][i];
-        }
-      }
-    }
+#if VRH_DECODE_SHARED_HINT
+  // Shared prefixes start at page 0: only rows whose first page is their
+  // neighbour's compare further pages (two uniform loads otherwise).
+  bool share_prev = false, share_next = false;
+  {
+    const int64_t table_rows = a.cu_q != nullptr ? (int64_t)a.num_seqs : a.rows;
+    const int first = table[0];
+    if (trow > 0) share_prev = table[-a.table_stride] == first;
+    if (trow + 1 < table_rows) share_next = table[a.table_stride] == first;
   }
+#endif
+
+  // The split loop is instantiated twice: with the per-page sharing test and,
+  // for rows that share no first page with a neighbour (all of a batch of
+  // independent prompts), without it, so that such rows run no extra
+  // instructions per chunk.
+  auto run = [&](auto hint_c) {
+    constexpr bool kHint = decltype(hint_c)::value;
+    for (int split = split0; split < P.nsplit; split += step) {
+      const int b0 = P.first + split * P.bps;
+      const int b1 = min(b0 + P.bps, P.first + P.pages);
+      const int tb = max(P.start, b0 * a.block_size);
+      const int te = min(n, b1 * a.block_size);
+
+      float m[HPW], l[HPW];
+      float acc[HPW][VEC];
+#pragma unroll
+      for (int h = 0; h < HPW; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.f;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[h][i] = 0.f;
+      }
+
+      for (int seg = b0; seg < b1; seg += 64) {
+        const bool in_seg = seg + lane < b1;
+        const int tbl = in_seg ? table[seg + lane] : 0;
+        const int s_tb = max(tb, seg * a.block_size);
+        const int s_te = min(te, (seg + 64) * a.block_size);
+        if (s_tb >= s_te) continue;
+#if VRH_DECODE_SHARED_HINT
+        // Pages this row shares with a neighbouring row of the batch (the same
+        // block at the same table index: parallel samples of one prompt, batches
+        // grouped by prefix) are read with ordinary loads, so that the rows'
+        // waves, dispatched together, find them in L2; other pages stream with
+        // non-temporal loads. Only the cache policy depends on this.
+        uint64_t shared_pages = 0;
+        if constexpr (kHint) {
+          bool shared = false;
+          if (in_seg && share_prev) shared = table[seg + lane - a.table_stride] == tbl;
+          if (in_seg && share_next) shared |= table[seg + lane + a.table_stride] == tbl;
+          shared_pages = __ballot(shared);
+        }
+#endif
+        // Branch-free loads: positions past the end re-read the last valid token
+        // (masked out of the softmax), so a chunk is one straight run of loads.
+        auto issue = [&](int p0, raw_t (&kr)[U], raw_t (&vr)[U], auto stream_c) {
+          constexpr bool kStream = decltype(stream_c)::value;
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int pos = min(p0 + u * TPL + tg, s_te - 1);
+            int page, off;
+            if (a.bs_shift >= 0) {
+              page = pos >> a.bs_shift;
+              off = pos & (a.block_size - 1);
+            } else {
+              page = pos / a.block_size;
+              off = pos - page * a.block_size;
+            }
+            const int64_t blk = shfl_i32(tbl, page - seg);
+            if constexpr (kStream) {
+              kr[u] = load_kv<T, VEC>(kbase + blk * a.k_block + (int64_t)off * a.k_token);
+              vr[u] = load_kv<T, VEC>(vbase + blk * a.v_block + (int64_t)off * a.v_token);
+            } else {
+              kr[u] = load_raw<T, VEC>(kbase + blk * a.k_block + (int64_t)off * a.k_token);
+              vr[u] = load_raw<T, VEC>(vbase + blk * a.v_block + (int64_t)off * a.v_token);
+            }
+          }
+        };
+        // The chunk at p0 is read with ordinary loads when one of its pages is
+        // shared with a neighbouring row (wave-uniform).
+        auto load_chunk = [&](int p0, raw_t (&kr)[U], raw_t (&vr)[U]) {
+#if VRH_DECODE_SHARED_HINT
+          if constexpr (kHint) {
+            const int last = min(p0 + CH, s_te) - 1;
+            int lo, hi;
+            if (a.bs_shift >= 0) {
+              lo = (p0 >> a.bs_shift) - seg;
+              hi = (last >> a.bs_shift) - seg;
+            } else {
+              lo = p0 / a.block_size - seg;
+              hi = last / a.block_size - seg;
+            }
+            const uint64_t span = hi - lo >= 63 ? ~0ull : ((2ull << (hi - lo)) - 1);
+            if ((shared_pages >> lo) & span) {
+              issue(p0, kr, vr, std::false_type{});
+              return;
+            }
+          }
+#endif
+          issue(p0, kr, vr, std::true_type{});
+        };
+        raw_t kr[U], vr[U];
+        load_chunk(s_tb, kr, vr);
+        for (int p0 = s_tb; p0 < s_te; p0 += CH) {
+#if VRH_DECODE_PREFETCH
+          raw_t kn[U], vn[U];
+          if (p0 + CH < s_te) load_chunk(p0 + CH, kn, vn);
+#endif
+          float sc[HPW][U];
+          float mx[HPW];
+#pragma unroll
+          for (int h = 0; h < HPW; ++h) mx[h] = m[h];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            float kf[VEC];
+            if constexpr (!kDot2) unpack<T, VEC>(kr[u], kf);
+            const bool visible = p0 + u * TPL + tg < s_te;
+#pragma unroll
+            for (int h = 0; h < HPW; ++h) {
+              float d = 0.f;
+              if constexpr (kDot2) {
+#pragma unroll
+                for (int i = 0; i < VEC / 2; ++i)
+                  d = __builtin_amdgcn_fdot2_f32_bf16(
+                      __builtin_bit_cast(bf16x2_t, qp2[h][i]),
+                      __builtin_bit_cast(bf16x2_t, (uint32_t)kr[u][i]), d, false);
+                d = group_sum<LPT>(d) * a.scale_log2;
+              } else {
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) d = fmaf(qf[h][i], kf[i], d);
+                d = group_sum<LPT>(d);
+              }
+              sc[h][u] = visible ? d : -INFINITY;
+              mx[h] = fmaxf(mx[h], sc[h][u]);
+            }
+          }
+          float safe[HPW];
+#pragma unroll
+          for (int h = 0; h < HPW; ++h) {
+            safe[h] = (mx[h] == -INFINITY) ? 0.f : mx[h];
+            const float corr = fast_exp2(m[h] - safe[h]);
+            l[h] *= corr;
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) acc[h][i] *= corr;
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            float vf[VEC];
+            unpack<T, VEC>(vr[u], vf);
+#pragma unroll
+            for (int h = 0; h < HPW; ++h) {
+              const float p = fast_exp2(sc[h][u] - safe[h]);
+              l[h] += p;
+#pragma unroll
+              for (int i = 0; i < VEC; ++i) acc[h][i] = fmaf(p, vf[i], acc[h][i]);
+            }
+          }
+#pragma unroll
+          for (int h = 0; h < HPW; ++h) m[h] = mx[h];
+#if VRH_DECODE_PREFETCH
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            kr[u] = kn[u];
+            vr[u] = vn[u];
+          }
+#else
+          if (p0 + CH < s_te) load_chunk(p0 + CH, kr, vr);
+#endif
+        }
+      }
+
+#pragma unroll
+      for (int h = 0; h < HPW; ++h) {
+        // Merge the token groups' states (fixed butterfly order).
+        const float M = cross_group_max<LPT>(m[h]);
+        const float w = (m[h] == -INFINITY) ? 0.f : fast_exp2(m[h] - M);
+        const float L = cross_group_sum<LPT>(l[h] * w);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[h][i] = cross_group_sum<LPT>(acc[h][i] * w);
+
+        if (P.nsplit == 1) {
+          if (tg == 0 && dvalid) {
+            const float inv = fast_rcp(fmaxf(L, 1e-30f));
+            float o[VEC];
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) o[i] = acc[h][i] * inv;
+            store_raw<T, VEC>(out + h * a.o_head, pack<T, VEC>(o));
+          }
+        } else {
+          const int64_t idx = ((row * a.q_heads + head0 + h) * kMaxSplits) + split;
+          if (lane == 0) {
+            a.part_ml[idx * 2 + 0] = M;
+            a.part_ml[idx * 2 + 1] = L;
+          }
+          if (tg == 0 && dvalid) {
+            float* dst = a.part_acc + idx * a.head_dim + dg * VEC;
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) dst[i] = acc[h][i];
+          }
+        }
+      }
+    }
+  };
+#if VRH_DECODE_SHARED_HINT
+  if (share_prev || share_next) {
+    run(std::true_type{});
+    return;
+  }
+#endif
+  run(std::false_type{});
 }
 
 // Grid slot of this wave: its row (after the longest-first ranking) and its
