@@ -168,9 +168,18 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
 // neither waits for it nor orders LDS reads behind it: the caller bounds it
 // with vm_wait before reading the LDS it fills. The s_nop is the wait state an
 // LDS-direct load needs after an M0 write (the compiler inserts it for the
-// instructions it knows, not inside asm).
+// instructions it knows, not inside asm). sc1 (agent scope) reads the line
+// from L2 without allocating it in the CU's L1: staged tiles are read once
+// per workgroup, so L1 allocation only adds tag work to the gather path.
 __device__ __forceinline__ void lds_dma16(const void* g, uint32_t m0) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(g), "{m0}"(m0) : "memory");
+}
+
+// The same load with a wave-uniform 64-bit base in SGPRs and a 32-bit byte
+// offset per lane (the saddr form: no 64-bit per-lane address).
+__device__ __forceinline__ void lds_dma16_s(const void* base, uint32_t lane_off, uint32_t m0) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 sc1" ::"v"(lane_off), "s"(base), "{m0}"(m0)
+               : "memory");
 }
 
 // s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt not waited on).

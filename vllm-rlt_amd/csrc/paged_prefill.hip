@@ -282,6 +282,14 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
   const T* lane_k1 = kg + (int64_t)lane_in * a.k_token + lane_dof;
   const T* lane_v1 = vg + (int64_t)lane_in * a.v_token + lane_dof;
   struct Regs { u32x4 k[NI]; u32x4 v[NI]; };
+#ifndef VRH_PREFILL_SADDR
+#define VRH_PREFILL_SADDR 1
+#endif
+  // Byte offset of this lane's 16 bytes within one staging instruction's rows
+  // (same for K and V when their strides match); 32-bit when it fits.
+  const int64_t lane_koff64 = ((int64_t)lane_in * a.k_token + lane_dof) * (int64_t)sizeof(T);
+  const bool lane_off32 = (int64_t)(IR - 1) * a.k_token * (int64_t)sizeof(T) + 2 * D < (1ll << 31);
+  const uint32_t lane_koff = (uint32_t)lane_koff64;
   // Addresses of sub-block j's K and V vectors for this wave's staging
   // instructions r = 0 .. NI - 1, handed to `sink(r, k_ptr, v_ptr)`.
   auto gather_to = [&](int j, auto&& sink) {
@@ -351,6 +359,26 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
     constexpr int stage = decltype(stage_c)::value;
     const uint32_t kl = lds_offset(ks[stage]) + 1024 * wave;
     const uint32_t vl = lds_offset(vs[stage]) + 1024 * wave;
+#if VRH_PREFILL_SADDR
+    const int k0 = j * kSB;
+    if (kPow2 && a.uniform_pages && a.same_kv32 && lane_off32 && k0 + kSB <= end) {
+      {
+        const int last_page = page_of(k0 + kSB - 1);
+        if (last_page >= tbl_base + kTableSeg) load_table(page_of(k0));
+      }
+#pragma unroll
+      for (int r = 0; r < NI; ++r) {
+        const int inst = wave + kWaves * r;
+        const int pb = k0 + IR * inst;
+        const uint32_t page = __builtin_amdgcn_readfirstlane(tbl_lds[(pb >> a.bs_shift) - tbl_base]);
+        const uint32_t row_off = __builtin_amdgcn_readfirstlane(pb & (a.block_size - 1));
+        const uint64_t off = (uint64_t)page * (uint32_t)a.k_block + (uint64_t)row_off * (uint32_t)a.k_token;
+        lds_dma16_s(kg + off, lane_koff, __builtin_amdgcn_readfirstlane(kl + 1024 * kWaves * r));
+        lds_dma16_s(vg + off, lane_koff, __builtin_amdgcn_readfirstlane(vl + 1024 * kWaves * r));
+      }
+      return;
+    }
+#endif
     gather_to(j, [&](int r, const T* kp, const T* vp) {
       lds_dma16(kp, __builtin_amdgcn_readfirstlane(kl + 1024 * kWaves * r));
       lds_dma16(vp, __builtin_amdgcn_readfirstlane(vl + 1024 * kWaves * r));
