@@ -398,3 +398,43 @@ def test_packed_prefill_fallback_ignores_padding_rows(gpu, dtype, head_dim):
     actual = paged_prefill_attention(padded, k, v, tables, lengths, cu, max_q)
     torch.cuda.synchronize()
     assert_close(actual[: q.shape[0]], oracle_prefill(q, k, v, tables, lengths, cu), dtype)
+
+
+@pytest.mark.parametrize("layout", ["same_pool", "pools_of_different_depth", "head_major_v"])
+@pytest.mark.parametrize("block", [16, 8])
+def test_packed_prefill_strided_kv_views(gpu, layout, block):
+    """MFMA prefill over K / V layer views whose strides differ from each other
+    (K and V from pools with different layer counts, or V stored head-major and
+    viewed as [N, bs, H, D]), against the per-query oracle; the staging then
+    forms separate K and V addresses instead of one shared offset."""
+    from vllm_rlt.kernels.hip_attention import paged_prefill_attention
+
+    sequences = [(2000, 300), (700, 129), (64, 64), (300, 1)]
+    heads, head_dim, dtype = 8, 128, torch.bfloat16
+    gen = torch.Generator().manual_seed(block + len(layout))
+    pages = sum(-(-n // block) for n, _ in sequences) + 3
+    if layout == "same_pool":
+        pool = torch.randn(pages, 2, 2, block, heads, head_dim, generator=gen).to(dtype).to(gpu)
+        k, v = pool[:, 0, 1], pool[:, 1, 1]
+    elif layout == "pools_of_different_depth":
+        kp = torch.randn(pages, 2, block, heads, head_dim, generator=gen).to(dtype).to(gpu)
+        vp = torch.randn(pages, 3, block, heads, head_dim, generator=gen).to(dtype).to(gpu)
+        k, v = kp[:, 1], vp[:, 2]
+    else:
+        k = torch.randn(pages, block, heads, head_dim, generator=gen).to(dtype).to(gpu)
+        v = torch.randn(pages, heads, block, head_dim, generator=gen).to(dtype).to(gpu)
+        v = v.permute(0, 2, 1, 3)
+    order = torch.randperm(pages, generator=gen).tolist()
+    width = max(-(-n // block) for n, _ in sequences)
+    tables = torch.full((len(sequences), width), -1, dtype=torch.int32)
+    for s, (n, _) in enumerate(sequences):
+        ids = [order.pop() for _ in range(-(-n // block))]
+        tables[s, : len(ids)] = torch.tensor(ids, dtype=torch.int32)
+    total = sum(c for _, c in sequences)
+    q = torch.randn(total, heads, head_dim, generator=gen).to(dtype).to(gpu)
+    cu = torch.tensor(np.cumsum([0] + [c for _, c in sequences]), dtype=torch.int32, device=gpu)
+    lengths = torch.tensor([n for n, _ in sequences], dtype=torch.int32, device=gpu)
+    tables = tables.to(gpu)
+    actual = paged_prefill_attention(q, k, v, tables, lengths, cu, 300)
+    expected = oracle_prefill(q, k.contiguous(), v.contiguous(), tables, lengths, cu)
+    assert_close(actual, expected, dtype)
