@@ -358,6 +358,15 @@ def test_empty_inputs(gpu):
     assert paged_attention(empty_q, k, k, tables, lengths).shape == (0, 2, 64)
     cu = torch.zeros(1, dtype=torch.int32, device=gpu)
     assert paged_prefill_attention(empty_q, k, k, tables, lengths, cu, 1).shape == (0, 2, 64)
+    # q heads not a multiple of kv heads (tests/test_attention.py:99-107)
+    q3 = torch.ones(1, 3, 64, device=gpu)
+    one_table = torch.zeros(1, 1, dtype=torch.int32, device=gpu)
+    one_length = torch.ones(1, dtype=torch.int32, device=gpu)
+    with pytest.raises(ValueError, match="positive multiple"):
+        paged_attention(q3, k, k, one_table, one_length)
+    with pytest.raises(ValueError, match="positive multiple"):
+        paged_prefill_attention(q3, k, k, one_table, one_length,
+                                torch.tensor([0, 1], dtype=torch.int32, device=gpu), 1)
 
 
 def test_prefill_without_workspace_runs_decode_rows_through_mfma_tiles(gpu):
