@@ -105,6 +105,10 @@ int vrh_kv_append(int dtype, void* key_cache, void* value_cache, int64_t cache_b
  * key_cache[block_tables[r, t / block_size], t % block_size]. Rows with n = 0
  * produce zeros. fp32 accumulation; the output is rounded to the storage dtype.
  * The result of a row depends only on that row's inputs (batch invariant).
+ * block_tables holds `rows` rows of table_width readable entries (row stride
+ * table_stride); entries past a row's ceil(n / block_size) pages are never used
+ * as page ids (they may be -1), but are compared with the neighbouring rows'
+ * entries at the same index, which only selects the cache policy of the loads.
  * `workspace` must hold vrh_paged_decode_workspace_bytes(rows, q_heads, head_dim)
  * bytes of device memory; it needs no initialisation. */
 size_t vrh_paged_decode_workspace_bytes(int64_t rows, int32_t q_heads, int32_t head_dim);
