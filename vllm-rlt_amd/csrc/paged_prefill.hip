@@ -106,6 +106,7 @@ struct PrefillArgs {
   int32_t uniform_pages;  // block size a power-of-two multiple of 256 / (16-byte chunks per row)
   int32_t same_kv32;      // K and V block/token strides equal and below 2^31
   const int32_t* order;   // sequences in dispatch order (longest first), or null
+  int32_t rank_in_kernel; // num_seqs <= 64: each wave ranks the sequences itself
   float scale_log2;
 };
 
@@ -191,18 +192,44 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
   const int64_t g = (slot / per_group) * 8 + blockIdx.x % 8;
   if (g >= a.num_seqs * a.kv_heads) return;
   const int r_item = (int)(slot % per_group);
-  const int64_t seq = a.order ? a.order[g / a.kv_heads] : g / a.kv_heads;
   const int head = (int)(g % a.kv_heads) * a.group + r_item / a.qblocks;
   const int qb = a.qblocks - 1 - r_item % a.qblocks;
   const int kvh = head / a.group;
-  const int q_begin = a.cu[seq];
-  const int q_len = a.cu[seq + 1] - q_begin;
-  if (qb * kBM >= q_len || q_len <= a.skip_q) return;
-  int n = a.lengths[seq];
-  {
-    const int64_t cap = (int64_t)a.table_width * a.block_size;
-    n = n < 0 ? 0 : ((int64_t)n > cap ? (int)cap : n);
+  const int64_t cap = (int64_t)a.table_width * a.block_size;
+  int64_t seq;
+  int q_begin, q_len, n;
+  if (a.rank_in_kernel) {
+    // Up to 64 sequences: every wave ranks them itself (one lane per
+    // sequence, the same longest-first stable order as prefill_order_kernel)
+    // and takes the sequence of rank g / kv_heads, without a separate launch.
+    const int s = lane;
+    int c0 = 0, c1 = 0, len = 0, key = INT32_MIN;
+    if (s < a.num_seqs) {
+      c0 = a.cu[s];
+      c1 = a.cu[s + 1];
+      len = a.lengths[s];
+      key = c1 - c0 <= a.skip_q ? -1 : (int)(len < 0 ? 0 : ((int64_t)len > cap ? cap : len));
+    }
+    int rank = 0;
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+      const int other = __builtin_amdgcn_readlane(key, j);
+      rank += (other > key) || (other == key && j < s);
+    }
+    const uint64_t hit = __ballot(rank == (int)(g / a.kv_heads) && s < a.num_seqs);
+    const int pick = __builtin_ffsll((long long)hit) - 1;
+    seq = pick;
+    q_begin = __builtin_amdgcn_readlane(c0, pick);
+    q_len = __builtin_amdgcn_readlane(c1, pick) - q_begin;
+    n = __builtin_amdgcn_readlane(len, pick);
+  } else {
+    seq = a.order ? a.order[g / a.kv_heads] : g / a.kv_heads;
+    q_begin = a.cu[seq];
+    q_len = a.cu[seq + 1] - q_begin;
+    n = a.lengths[seq];
   }
+  if (qb * kBM >= q_len || q_len <= a.skip_q) return;
+  n = n < 0 ? 0 : ((int64_t)n > cap ? (int)cap : n);
   const int prefix = n - q_len;
   const int qi0 = qb * kBM + wave * kWQ;        // this wave's first query
   const int qi = qi0 + col;                     // this lane's query
@@ -666,6 +693,9 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
 // j < i)}, so equal keys keep their order and the permutation is stable.
 // key = clamped length, or -1 for sequences the MFMA kernel skips.
 constexpr int kOrderMax = 2048;  // larger batches keep the identity order
+#ifndef VRH_PREFILL_RANK_IN_KERNEL
+#define VRH_PREFILL_RANK_IN_KERNEL 1
+#endif
 __global__ __launch_bounds__(1024) void prefill_order_kernel(const int32_t* cu, const int32_t* lengths,
                                                              int32_t num_seqs, int32_t skip_q,
                                                              int64_t cap, int32_t* order) {
@@ -811,7 +841,8 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   a.kv_heads = kv_heads;
   a.qblocks = ceil_div(max_seqlen_q, kBM);
   a.order = nullptr;
-  if (route_decode && num_seqs > 1 && num_seqs <= kOrderMax) {
+  a.rank_in_kernel = VRH_PREFILL_RANK_IN_KERNEL && route_decode && num_seqs > 1 && num_seqs <= 64;
+  if (route_decode && num_seqs > 1 && num_seqs <= kOrderMax && !a.rank_in_kernel) {
     int32_t* order = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
                                                 decode_part_bytes(num_seqs, q_heads, head_dim));
     hipLaunchKernelGGL(prefill_order_kernel, dim3(1), dim3(1024), 0, s, cu_seqlens_q,
