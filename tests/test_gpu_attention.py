@@ -447,3 +447,42 @@ def test_packed_prefill_strided_kv_views(gpu, layout, block):
     actual = paged_prefill_attention(q, k, v, tables, lengths, cu, 300)
     expected = oracle_prefill(q, k.contiguous(), v.contiguous(), tables, lengths, cu)
     assert_close(actual, expected, dtype)
+
+
+@pytest.mark.parametrize("count", [64, 65, 130])
+def test_packed_prefill_many_sequences(gpu, count):
+    """Batches ranked inside the MFMA kernel (up to 64 sequences) and by the
+    separate ordering kernel (more), with decode rows, short chunks and a few
+    long ones in one batch, against the per-query oracle."""
+    from vllm_rlt.kernels.hip_attention import paged_prefill_attention
+
+    gen = torch.Generator().manual_seed(count)
+    sequences = []
+    for s in range(count):
+        kind = s % 5
+        if kind == 0:
+            sequences.append((int(torch.randint(1, 400, (1,), generator=gen)), 1))
+        elif kind == 4 and s < 20:
+            n = int(torch.randint(300, 1200, (1,), generator=gen))
+            sequences.append((n, int(torch.randint(129, min(n, 400), (1,), generator=gen))))
+        else:
+            n = int(torch.randint(2, 200, (1,), generator=gen))
+            sequences.append((n, int(torch.randint(1, n + 1, (1,), generator=gen))))
+    block, heads = 16, 4
+    pages = sum(-(-n // block) for n, _ in sequences)
+    k = torch.randn(pages, block, heads, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    v = torch.randn(pages, block, heads, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    order = torch.randperm(pages, generator=gen).tolist()
+    width = max(-(-n // block) for n, _ in sequences)
+    tables = torch.full((count, width), -1, dtype=torch.int32)
+    for s, (n, _) in enumerate(sequences):
+        ids = [order.pop() for _ in range(-(-n // block))]
+        tables[s, : len(ids)] = torch.tensor(ids, dtype=torch.int32)
+    total = sum(c for _, c in sequences)
+    q = torch.randn(total, heads, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    cu = torch.tensor(np.cumsum([0] + [c for _, c in sequences]), dtype=torch.int32, device=gpu)
+    lengths = torch.tensor([n for n, _ in sequences], dtype=torch.int32, device=gpu)
+    tables = tables.to(gpu)
+    max_q = max(c for _, c in sequences)
+    actual = paged_prefill_attention(q, k, v, tables, lengths, cu, max_q)
+    assert_close(actual, oracle_prefill(q, k, v, tables, lengths, cu), torch.bfloat16)
