@@ -841,7 +841,9 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   a.kv_heads = kv_heads;
   a.qblocks = ceil_div(max_seqlen_q, kBM);
   a.order = nullptr;
-  a.rank_in_kernel = VRH_PREFILL_RANK_IN_KERNEL && route_decode && num_seqs > 1 && num_seqs <= 64;
+  // Up to 64 sequences are ranked inside the kernel (also without a
+  // workspace); larger batches use the ordering kernel and the workspace.
+  a.rank_in_kernel = VRH_PREFILL_RANK_IN_KERNEL && num_seqs > 1 && num_seqs <= 64;
   if (route_decode && num_seqs > 1 && num_seqs <= kOrderMax && !a.rank_in_kernel) {
     int32_t* order = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
                                                 decode_part_bytes(num_seqs, q_heads, head_dim));
