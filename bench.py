@@ -832,15 +832,34 @@ def main():
                                              pw.cu_seqlens_q, pw.max_seqlen_q)] * 4, replays=3)
         # Whole packed call: the 16 MFMA chunks plus the 48 decode rows, which
         # run through the HBM-bound split-KV kernel (0.86 GB of K/V).
+        # The call mixes MFMA work (the chunks) and HBM work (the decode rows'
+        # K/V): its roofline time is the sum of the two at their peaks.
+        cu, lens = pw.cu_seqlens_q.tolist(), pw.context_lengths.tolist()
+        heads, dim = pw.q.shape[1], pw.q.shape[2]
+        kv_heads, elt = pw.key_cache.shape[3], pw.key_cache.element_size()
+        chunk_flops = decode_row_bytes = 0
+        for s_, n_ in enumerate(lens):
+            q_len = cu[s_ + 1] - cu[s_]
+            if q_len > 1:
+                chunk_flops += 4 * dim * heads * sum(n_ - q_len + i + 1 for i in range(q_len))
+            else:
+                decode_row_bytes += n_ * 2 * kv_heads * dim * elt + 2 * heads * dim * elt
+        roofline_us = (chunk_flops / (BF16_PEAK_TFLOPS * 1e12)
+                       + decode_row_bytes / (HBM_PEAK_GBS * 1e9)) * 1e6
         extras["prefill_config4"] = {
             "tflops": round(flops / (prefill_ms * 1e-3) / 1e12, 2), "ms": round(prefill_ms, 4),
             "pct_of_bf16_mfma_peak": round(100 * flops / (prefill_ms * 1e-3) / 1e12
                                            / BF16_PEAK_TFLOPS, 2),
             "graph_ms": round(prefill_graph_ms, 4),
             "graph_tflops": round(flops / (prefill_graph_ms * 1e-3) / 1e12, 2),
-            "includes": "16 chunks (MFMA kernel) + 48 decode rows (split-KV decode kernel)"}
-        # The 16 chunks alone: the MFMA kernel (plus the ~2 us dispatch-order
-        # kernel), graph-timed.
+            "chunk_flops": chunk_flops, "decode_row_bytes": decode_row_bytes,
+            "roofline_us": round(roofline_us, 1),
+            "roofline_frac_graph": round(roofline_us / (prefill_graph_ms * 1e3), 4),
+            "includes": "16 chunks (MFMA kernel) + 48 decode rows (split-KV decode kernel); "
+                        "roofline_us = chunk FLOPs at the bf16 MFMA peak + decode-row bytes at "
+                        "the HBM peak"}
+        # The 16 chunks alone: the MFMA kernel (sequences ranked in-kernel) and
+        # the empty decode-row launch, graph-timed.
         del pw, kc, vc
         torch.cuda.empty_cache()
         pw = workloads.config4(device=device, decode_rows=0)
