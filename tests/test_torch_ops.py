@@ -6,8 +6,8 @@ CPU: the module loads through the reference's loader contract
 paged-KV ops, and has no CPU kernel (no silent host fallback).
 
 GPU: every op gives bit-identical results to the ctypes adapter over the same
-C entry point, and its checks raise RuntimeError (TORCH_CHECK), as the
-reference's native entry does (csrc/activation/silu_and_mul.cu:221-232).
+C entry point (also captured in a HIP graph and replayed), and its checks raise
+RuntimeError (TORCH_CHECK), as the reference's native entry does (csrc/activation/silu_and_mul.cu:221-232).
 """
 
 import pytest
@@ -167,3 +167,57 @@ def test_op_checks_raise_runtime_error(gpu):
     with pytest.raises(RuntimeError, match="one row per query row"):
         torch.ops.vllm_rlt_hip.paged_attention(q, cache, cache, tables[:1],
                                                torch.zeros(1, dtype=torch.int32, device=gpu))
+
+
+@pytest.mark.gpu
+def test_ops_in_a_captured_graph(gpu):
+    """The torch ops captured in one HIP graph (decode, prefill, append) and
+    replayed three times, with new inputs written in place and eager work in
+    between; every replay gives the eager result bit for bit."""
+    load_extension()
+    gen = torch.Generator().manual_seed(6)
+    kc, vc = _pool(gen, 128, 1, 16, 8, 128, torch.bfloat16, gpu)
+    k_view, v_view = kc[:, 0], vc[:, 0]
+    tables = torch.randperm(128, generator=gen)[:4 * 30].view(4, 30).to(torch.int32).to(gpu)
+    lengths = torch.tensor([300, 1, 450, 45], dtype=torch.int32, device=gpu)
+    cu = torch.tensor([0, 200, 201, 457, 502], dtype=torch.int32, device=gpu)
+    q_dec = torch.empty(4, 16, 128, dtype=torch.bfloat16, device=gpu)
+    q_pre = torch.empty(502, 16, 128, dtype=torch.bfloat16, device=gpu)
+    k_new = torch.empty(4, 8, 128, dtype=torch.bfloat16, device=gpu)
+    v_new = torch.empty_like(k_new)
+    blocks = tables[:, 0].to(torch.int64)
+    offsets = torch.tensor([3, 0, 15, 7], dtype=torch.int64, device=gpu)
+
+    def fill(seed):
+        g = torch.Generator().manual_seed(seed)
+        q_dec.copy_(torch.randn(q_dec.shape, generator=g).to(torch.bfloat16))
+        q_pre.copy_(torch.randn(q_pre.shape, generator=g).to(torch.bfloat16))
+        k_new.copy_(torch.randn(k_new.shape, generator=g).to(torch.bfloat16))
+        v_new.copy_(torch.randn(v_new.shape, generator=g).to(torch.bfloat16))
+
+    def step():
+        torch.ops.vllm_rlt_hip.kv_append(k_view, v_view, k_new, v_new, blocks, offsets)
+        dec = torch.ops.vllm_rlt_hip.paged_attention(q_dec, k_view, v_view, tables, lengths, 0)
+        pre = torch.ops.vllm_rlt_hip.paged_prefill(q_pre, k_view, v_view, tables, lengths, cu, 256)
+        return dec, pre
+
+    fill(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        dec_out, pre_out = step()
+    for seed in (1, 2, 3):
+        fill(seed)
+        graph.replay()
+        torch.cuda.synchronize()
+        got_dec, got_pre = dec_out.clone(), pre_out.clone()
+        want_dec, want_pre = step()  # eager, same inputs (the append rewrites the same slots)
+        torch.cuda.synchronize()
+        assert torch.equal(got_dec, want_dec), seed
+        assert torch.equal(got_pre, want_pre), seed
+        hip.paged_attention(q_dec, k_view, v_view, tables, lengths)  # eager work in between
