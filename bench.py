@@ -59,7 +59,8 @@ def parse_args():
                         help="budget of the CPU baseline sample")
     parser.add_argument("--leg", choices=["prefill_config4", "prefill_chunks_config4",
                                           "append_config4", "decode_config2",
-                                          "decode_config5", "decode_gqa", "movers"],
+                                          "decode_config3", "decode_config5", "decode_gqa",
+                                          "movers"],
                         help="run only this workload (for profiling) and print its timing")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run vrh_kv_copy_blocks over a known byte count (the "
@@ -627,6 +628,15 @@ def single_leg(name, repeats):
     elif name == "decode_config5":
         print(json.dumps({"leg": name, **decode_config5_leg(device, calls=repeats)}),
               flush=True)
+    elif name == "decode_config3":
+        w = workloads.config3(device=device)
+        k, v = w.key_cache[:, 0], w.value_cache[:, 0]
+        ms = event_time_ms(lambda: paged_attention(w.q, k, v, w.block_tables,
+                                                   w.context_lengths), repeats)
+        es = w.key_cache.element_size()
+        unique = w.extra["unique_tokens"] * 2 * w.key_cache.shape[3] * w.key_cache.shape[4] * es
+        print(json.dumps({"leg": name, "us": round(ms * 1e3, 2), "per_row_bytes": w.decode_bytes(),
+                          "unique_kv_bytes": unique}), flush=True)
 
 
 def main():
