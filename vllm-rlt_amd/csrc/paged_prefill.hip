@@ -396,6 +396,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
 #pragma unroll
       for (int r = 0; r < NI; ++r) {
         const int inst = wave + kWaves * r;
+        if (SB_INST % kWaves != 0 && inst >= SB_INST) continue;  // no such instruction
         const int pb = k0 + IR * inst;
         const uint32_t page = __builtin_amdgcn_readfirstlane(tbl_lds[(pb >> a.bs_shift) - tbl_base]);
         const uint32_t row_off = __builtin_amdgcn_readfirstlane(pb & (a.block_size - 1));
@@ -565,13 +566,23 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
   using H2 = std::integral_constant<int, 2>;
   using H3 = std::integral_constant<int, 3>;
   f32x16 st = f32x16{};
-  // LDS-direct staging (sub-block j + 3 loaded into LDS at step j: two steps
-  // of load latency) where every wave issues the same number of staging
-  // loads per sub-block, so that one vmcnt bound fits every wave; otherwise
-  // staging through registers (sub-block j + 3 gathered at step j, stored at
-  // step j + 1).
-  constexpr bool kDma = VRH_PREFILL_DMA && kStages == 4 && SB_INST % kWaves == 0;
+  // LDS-direct staging: sub-block j + 3 loaded into LDS at step j (two steps
+  // of load latency). With it switched off, staging goes through registers
+  // (sub-block j + 3 gathered at step j, stored at step j + 1).
+#ifndef VRH_PREFILL_DMA_UNEVEN
+#define VRH_PREFILL_DMA_UNEVEN 1
+#endif
+  constexpr bool kDma = VRH_PREFILL_DMA && kStages == 4 &&
+                        (VRH_PREFILL_DMA_UNEVEN || SB_INST % kWaves == 0);
   constexpr int kDmaPerStep = 2 * NI;  // K and V loads per wave per sub-block
+  // Where the staging loads do not divide evenly (head dims 32 and 96), the
+  // first SB_INST % kWaves waves issue NI loads of K and of V per sub-block
+  // and the others NI - 1: each wave bounds vmcnt by its own count.
+  const bool full_share = SB_INST % kWaves == 0 || wave < SB_INST % kWaves;
+  auto dma_wait_newest = [&]() {  // every sub-block but the newest has landed
+    if (full_share) vm_wait<kDmaPerStep>();
+    else vm_wait<2 * (NI - 1)>();
+  };
   Regs R;
   if (nsub > 0) {
     if constexpr (kDma) {
@@ -579,7 +590,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
       if (nsub > 1) dma(1, H1{});
       if (nsub > 2) {
         dma(2, H2{});
-        vm_wait<kDmaPerStep>();  // sub-blocks 0 and 1 have landed
+        dma_wait_newest();  // sub-blocks 0 and 1 have landed
       } else {
         vm_wait<0>();
       }
@@ -605,7 +616,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
         // loads of j + 2 (issued one step ago) may still be in flight. The
         // barrier then publishes it and frees the stage of j - 1 for j + 3.
         using Hd = std::integral_constant<int, (h + 3) % kStages>;
-        if (j + 2 < nsub) vm_wait<kDmaPerStep>();
+        if (j + 2 < nsub) dma_wait_newest();
         else vm_wait<0>();
         __syncthreads();
         if (j + 3 < nsub) dma(j + 3, Hd{});
