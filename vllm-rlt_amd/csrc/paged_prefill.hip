@@ -9,9 +9,8 @@
 // MFMA path (bf16/f16, head_dim a multiple of 32 up to 128):
 //  * Workgroup = 4 waves = 128 query rows of one (sequence, q head); each wave
 //    owns 32 queries. K/V arrive in 32-key sub-blocks staged into LDS (four
-//    stages; loaded straight into LDS three sub-blocks ahead, or through
-//    registers where the waves' staging loads do not divide evenly) and
-//    shared by the 4 waves; one barrier per sub-block.
+//    stages, loaded straight into LDS three sub-blocks ahead) and shared by
+//    the 4 waves; one barrier per sub-block.
 //  * Each wave software-pipelines the sub-blocks: the QK^T MFMAs of sub-block
 //    j + 1 are interleaved with the softmax VALU work of sub-block j.
 //  * S^T = K Q^T with v_mfma_f32_32x32x16_{bf16,f16}: A = K rows from LDS
