@@ -66,6 +66,9 @@ namespace {
 #endif
 constexpr int kMaxSplits = VRH_MAX_SPLITS;
 constexpr int kSplitTokens = VRH_SPLIT_TOKENS;  // minimum tokens per split (whole pages)
+#ifndef VRH_DECODE_LINE_SHARED
+#define VRH_DECODE_LINE_SHARED 1
+#endif
 #ifndef VRH_DECODE_SHARED_HINT
 #define VRH_DECODE_SHARED_HINT 1
 #endif
@@ -100,6 +103,10 @@ struct DecodeArgs {
   int64_t table_stride;
   int64_t row_base;
   int64_t rows;      // rows of the whole call (the launch may cover a chunk)
+  // A head's row of K or V is not a whole number of 128-byte cache lines, so
+  // neighbouring heads (other waves) share lines: every page is then read
+  // with cache-allocating loads.
+  int32_t line_shared;
   // Packed-prefill expansion (null for decode): row r is query i of sequence
   // s with cu_q[s] <= r < cu_q[s+1]; it reads table row s with causal length
   // lengths[s] - q_len(s) + i + 1.
@@ -305,7 +312,7 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
           bool shared = false;
           if (in_seg && share_prev) shared = table[seg + lane - a.table_stride] == tbl;
           if (in_seg && share_next) shared |= table[seg + lane + a.table_stride] == tbl;
-          shared_pages = __ballot(shared);
+          shared_pages = a.line_shared ? ~0ull : __ballot(shared);
         }
 #endif
         // Branch-free loads: positions past the end re-read the last valid token
@@ -459,7 +466,7 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
     }
   };
 #if VRH_DECODE_SHARED_HINT
-  if (share_prev || share_next) {
+  if (share_prev || share_next || a.line_shared) {
     run(std::true_type{});
     return;
   }
@@ -1010,6 +1017,7 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.window = window;
   a.table_width = table_width;
+  a.line_shared = VRH_DECODE_SHARED_HINT && VRH_DECODE_LINE_SHARED && ((int64_t)head_dim * es) % 128 != 0;
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
   // Pages per split: at least kSplitTokens tokens; without a workspace every
   // row is a single split (pages can never exceed the table width).
