@@ -878,12 +878,35 @@ def main():
             [lambda: paged_prefill_attention(pw.q, kc, vc, pw.block_tables, pw.context_lengths,
                                              pw.cu_seqlens_q, pw.max_seqlen_q)] * 4, replays=3)
         chunk_flops = pw.flops()
+        # The same chunks through the C ABI without a workspace (a caller that
+        # knows its batch has no one-query sequences): no decode-row launch,
+        # so the call is the MFMA kernel alone.
+        lib = library()
+        out_nows = torch.empty_like(pw.q)
+
+        def chunks_no_workspace():
+            lib.check(lib.vrh_paged_prefill(
+                2, out_nows.data_ptr(), pw.q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                pw.block_tables.data_ptr(), pw.context_lengths.data_ptr(),
+                pw.cu_seqlens_q.data_ptr(), pw.block_tables.shape[0], pw.q.shape[0],
+                int(pw.max_seqlen_q), pw.q.shape[1], kc.shape[2], pw.q.shape[2], kc.shape[1],
+                pw.block_tables.shape[1], pw.block_tables.stride(0), pw.q.stride(0),
+                pw.q.stride(1), out_nows.stride(0), out_nows.stride(1), *kc.stride()[:3],
+                *vc.stride()[:3], None, 0, torch.cuda.current_stream().cuda_stream),
+                "vrh_paged_prefill")
+
+        kernel_ms = graph_time_ms([chunks_no_workspace] * 4, replays=3)
         extras["prefill_config4_chunks_mfma"] = {
             "graph_ms": round(chunks_ms, 4),
             "tflops": round(chunk_flops / (chunks_ms * 1e-3) / 1e12, 2),
             "pct_of_bf16_mfma_peak": round(100 * chunk_flops / (chunks_ms * 1e-3) / 1e12
                                            / BF16_PEAK_TFLOPS, 2),
-            "flops": chunk_flops}
+            "flops": chunk_flops,
+            "kernel_only_graph_ms": round(kernel_ms, 4),
+            "kernel_only_pct_of_bf16_mfma_peak": round(
+                100 * chunk_flops / (kernel_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 2),
+            "kernel_only": "same chunks through vrh_paged_prefill with no workspace: the "
+                           "MFMA kernel alone (no decode-row launch and merge)"}
         # Hidden-state segments of the config-4 chunks around prefill: gather the
         # 16 x 512 chunk rows (Ouro hidden 2048, bf16) from the state pool.
         chunk_rows = pw.chunk_sequences * 512
