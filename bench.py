@@ -33,11 +33,11 @@ HBM_PEAK_GBS = 8000.0
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_decode_config2.md")
 
 
-def profiled_traffic():
-    """HBM bytes per decode call from the committed rocprof PMC summary (scaled
-    FETCH_SIZE + WRITE_SIZE of the split and merge kernels), or None."""
+def profiled_traffic(path=TRAFFIC_PROFILE):
+    """HBM bytes per call from a committed rocprof PMC summary (scaled
+    FETCH_SIZE + WRITE_SIZE of the call's kernels), or None."""
     try:
-        for line in open(TRAFFIC_PROFILE):
+        for line in open(path):
             if line.startswith("traffic_bytes_per_call:"):
                 return int(line.split(":")[1])
     except OSError:
@@ -58,7 +58,7 @@ def parse_args():
     parser.add_argument("--cpu-seconds", type=float, default=10.0,
                         help="budget of the CPU baseline sample")
     parser.add_argument("--leg", choices=["prefill_config4", "prefill_chunks_config4",
-                                          "append_config4", "decode_config2",
+                                          "append_config4", "append_config2", "decode_config2",
                                           "decode_config3", "decode_config5", "decode_gqa",
                                           "movers"],
                         help="run only this workload (for profiling) and print its timing")
@@ -486,6 +486,21 @@ def rotating_append_layers(work, sets=48):
     return fns, work.append_bytes(work.layers), (k_sets, v_sets, blocks, offsets)
 
 
+def plain_copy_floor(nbytes_moved, device, sets=48):
+    """Graph-timed ``dst.copy_(src)`` of contiguous tensors moving the same
+    bytes (half read, half written) over ``sets`` rotating pairs: the time any
+    kernel needs to move that many bytes in one launch on this chip."""
+    import torch
+
+    elems = nbytes_moved // 2 // 2  # bf16 elements read (= written)
+    src = [torch.empty(elems, dtype=torch.bfloat16, device=device).normal_()
+           for _ in range(sets)]
+    dst = [torch.empty_like(x) for x in src]
+    ms = graph_time_ms([lambda i=i: dst[i].copy_(src[i]) for i in range(sets)], replays=2)
+    del src, dst
+    return ms
+
+
 def decode_config5_leg(device, calls=6):
     """Config 5's decode shape: 256 rows, context U[2048, 32768], over one layer
     view of a 48-layer pool of 32768 blocks (6 MiB of K+V per block: 192 GiB,
@@ -501,10 +516,22 @@ def decode_config5_leg(device, calls=6):
     call = lambda: paged_attention(w.q, kc, vc, w.block_tables, w.context_lengths)  # noqa: E731
     ms = graph_time_ms([call] * calls, replays=2)
     nbytes = w.decode_bytes()
+    tokens = int(w.context_lengths.sum())
+    slots = w.num_blocks * w.key_cache.shape[2]
     out = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 2), "ms": round(ms, 4),
            "pct_of_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
            "bytes_per_call": nbytes, "rows": w.rows, "pool_blocks": w.num_blocks,
-           "tokens": int(w.context_lengths.sum())}
+           "tokens": tokens, "page_reuse": round(tokens / slots, 2),
+           "bytes": "gbs counts K/V once per row that reads it (rows share random pages, "
+                    f"{tokens} tokens over {slots} slots)"}
+    traffic = profiled_traffic(os.path.join(ROOT, "profiles", "paged_decode_config5.md"))
+    if traffic:
+        # HBM bytes per call measured by FETCH_SIZE / WRITE_SIZE (scaled by a
+        # calibration copy): the rate on bytes the memory actually delivered.
+        out["traffic_bytes_per_call"] = traffic
+        out["gbs_counter_bytes"] = round(traffic / (ms * 1e-3) / 1e9, 2)
+        out["pct_of_hbm_peak_counter_bytes"] = round(
+            100 * traffic / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
     del w, kc, vc
     torch.cuda.empty_cache()
     return out
@@ -603,6 +630,12 @@ def single_leg(name, repeats):
         print(json.dumps({"leg": name, "us": round(ms * 1e3, 2), "bytes_per_call": nbytes,
                           "rows": rows, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2)}),
               flush=True)
+    elif name == "append_config2":
+        w = workloads.config2(device=device)
+        fns, nbytes, _keep = rotating_append_layers(w)
+        ms = event_time_ms(lambda: [fn() for fn in fns], repeats) / len(fns)
+        print(json.dumps({"leg": name, "us": round(ms * 1e3, 2), "bytes_per_call": nbytes,
+                          "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2)}), flush=True)
     elif name == "decode_config2":
         w = workloads.config2(device=device)
         layers = [(w.key_cache[:, l], w.value_cache[:, l]) for l in range(w.layers)]
@@ -780,6 +813,7 @@ def main():
         fns, append_layers_bytes, keep = rotating_append_layers(work)
         append_layers_ms = graph_time_ms(fns, replays=2)
         del keep, fns
+        copy_floor_ms = plain_copy_floor(append_layers_bytes, device)
         # single-layer decode append (latency)
         single_ms = graph_time_ms(
             [lambda layer=layer: kv_append(kviews[layer], vviews[layer], work.k_new[layer],
@@ -795,7 +829,11 @@ def main():
                 "us": round(append_layers_ms * 1e3, 2), "bytes": append_layers_bytes,
                 "pct_of_hbm_peak": round(100 * append_layers_bytes / (append_layers_ms * 1e-3)
                                          / 1e9 / HBM_PEAK_GBS, 2),
-                "rotation": "48 disjoint input/destination sets, 1.2 GB"},
+                "rotation": "48 disjoint input/destination sets, 1.2 GB",
+                "plain_copy_same_bytes_us": round(copy_floor_ms * 1e3, 2),
+                "vs_plain_copy": round(copy_floor_ms / append_layers_ms, 3),
+                "plain_copy": "torch copy_ of contiguous tensors moving the same bytes, "
+                              "48 rotating pairs, graph-timed"},
             "append_one_layer_us": round(single_ms * 1e3, 2),
             "append_one_layer_gbs": round(work.append_bytes(1) / (single_ms * 1e-3) / 1e9, 2)}
         extras.update(pool_movers(work))

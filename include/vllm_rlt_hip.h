@@ -4,7 +4,9 @@
  * One shared library (libvllm_rlt_hip.so) exports these entry points. They take
  * plain device pointers, element strides (int64, in elements of the storage
  * dtype unless the name says bytes) and a hipStream_t, launch asynchronously on
- * that stream, never synchronise and never allocate device memory. They return
+ * that stream, never synchronise and never allocate device memory (the one
+ * standing reservation is the 96 MiB per-GPU array of vrh_paged_decode_noalloc,
+ * made when the library's code object loads on a GPU). They return
  * VRH_OK or an error code; vrh_last_error() then holds a message for the
  * calling thread.
  *
@@ -87,6 +89,9 @@ const char* vrh_last_error(void);
  * (write_mask == NULL || write_mask[r] != 0). Disabled rows are not touched.
  * `layers` > 1 batches the appends of several layers (k/v layer strides and
  * the cache layer stride select them); pass layers = 1 for one layer view.
+ * With num_blocks > 0 (block_size > 0), a row whose block id lies outside
+ * [0, num_blocks) (offset outside [0, block_size)) writes nothing, so a bad
+ * address cannot write outside the pool; pass 0 to leave them unchecked.
  * Bit-exact copy. */
 int vrh_kv_append(int dtype, void* key_cache, void* value_cache, int64_t cache_block_stride,
                   int64_t cache_token_stride, int64_t cache_head_stride,
@@ -95,7 +100,8 @@ int vrh_kv_append(int dtype, void* key_cache, void* value_cache, int64_t cache_b
                   int64_t v_head_stride, int64_t v_layer_stride, const int64_t* write_blocks,
                   const int64_t* write_offsets, const uint8_t* write_mask,
                   const int32_t* active_rows, int64_t rows, int32_t layers, int32_t kv_heads,
-                  int32_t head_dim, vrh_stream_t stream);
+                  int32_t head_dim, int64_t num_blocks, int32_t block_size,
+                  vrh_stream_t stream);
 
 /* ------------------------------------------------------------ paged decode
  * Single-query attention per row over its own block table:
@@ -133,7 +139,13 @@ int vrh_paged_decode(int dtype, void* out, const void* q, const void* key_cache,
  * more than 756 rows x 16 heads at head_dim 128) fail with
  * VRH_ERROR_INVALID_ARG before any launch. Every call on one GPU shares that
  * array: calls that overlap on one GPU (other streams, concurrent graph
- * replays) race. Nothing in it needs clearing between calls. */
+ * replays) race. Nothing in it needs clearing between calls.
+ * Fixed cost: the array is part of the library's code object, so its 96 MiB
+ * are reserved on every GPU where the library is loaded, whether or not this
+ * entry point is ever called (a caller sizing its KV pool to the last GiB
+ * counts them). vrh_paged_decode_noalloc_max_bytes() also looks up the
+ * current device's array address (once per device): a caller that captures
+ * calls into a HIP graph calls it on each device before capture. */
 #define VRH_PAGED_DECODE_NOALLOC_MAX_BYTES ((size_t)96 << 20)
 size_t vrh_paged_decode_noalloc_max_bytes(void);
 int vrh_paged_decode_noalloc(int dtype, void* out, const void* q, const void* key_cache,
@@ -154,13 +166,20 @@ int vrh_paged_decode_noalloc(int dtype, void* out, const void* q, const void* ke
  * at positions <= that. bf16/f16 with head_dim 32, 64, 96 or 128 (and
  * 16-byte aligned rows) use MFMA tiles with fp32 accumulation; other cases
  * compute each query row with the decode kernel. With a workspace of
- * vrh_paged_prefill_workspace_bytes(num_seqs, q_heads, head_dim) bytes,
- * sequences of one query (decode rows riding in a packed batch) use split-KV
- * decode, and the MFMA work items are dispatched longest sequence first (a
- * small ranking kernel writes the order into the workspace; batches of up to
- * 2048 sequences). With none (NULL, 0) every sequence goes through the MFMA
- * tiles in batch order. Results do not depend on the order. */
-size_t vrh_paged_prefill_workspace_bytes(int64_t num_seqs, int32_t q_heads, int32_t head_dim);
+ * vrh_paged_prefill_workspace_bytes(num_seqs, max_seqlen_q, q_heads, head_dim)
+ * bytes, sequences of one query (decode rows riding in a packed batch) use
+ * split-KV decode, and the MFMA work items are dispatched longest sequence
+ * first (batches of up to 64 sequences are ranked inside the kernel, larger
+ * ones up to 2048 by a small ranking kernel writing the order into the
+ * workspace). With none (NULL, 0) every sequence goes through the MFMA tiles
+ * in batch order. Results do not depend on the order.
+ * Decode exactness (the reference's packed_matches_decode, attention/backend.py:
+ * 21-23): with the workspace and max_seqlen_q <= 8, every query runs as its own
+ * split-KV decode row, and query i of sequence s equals, bit for bit, what
+ * vrh_paged_decode returns for a row with the same q, table row and length
+ * n_s - q_s + i + 1 (the decode partition depends only on that length). */
+size_t vrh_paged_prefill_workspace_bytes(int64_t num_seqs, int32_t max_seqlen_q, int32_t q_heads,
+                                         int32_t head_dim);
 int vrh_paged_prefill(int dtype, void* out, const void* q, const void* key_cache,
                       const void* value_cache, const int32_t* block_tables,
                       const int32_t* context_lengths, const int32_t* cu_seqlens_q,

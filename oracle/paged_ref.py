@@ -111,6 +111,40 @@ def paged_prefill(q, key_cache, value_cache, block_tables, context_lengths, cu_s
 
 
 # ------------------------------------------------------------- KV writes
+def causal_block(q, keys, values, positions):
+    """Query rows of one sequence over its contiguous history, vectorised.
+
+    ``keys``/``values`` ``[n, Hkv, D]`` are the sequence's keys in position
+    order (the pages already gathered), ``q`` ``[m, Hq, D]``, and query j sees
+    keys ``0 .. positions[j]``: the same arithmetic as :func:`paged_attention`
+    on rows of length ``positions[j] + 1`` (fp32 scores scaled by 1/sqrt(D),
+    softmax, weighted V; GQA head h reads kv head h // (Hq / Hkv)), with one
+    matrix product per head instead of a loop over rows. Used to check whole
+    query tiles of the packed prefill (triton_attention.py:241-263,281).
+    Returns float32 ``[m, Hq, D]``.
+    """
+    q = np.asarray(q, dtype=np.float32)
+    rows, heads, dim = q.shape
+    keys = np.asarray(keys, dtype=np.float32)
+    values = np.asarray(values, dtype=np.float32)
+    groups = heads // keys.shape[1]
+    positions = np.asarray(positions, dtype=np.int64)
+    scale = np.float32(1.0 / math.sqrt(dim))
+    n = int(positions.max()) + 1 if rows else 0
+    visible = np.arange(n)[None, :] <= positions[:, None]  # [m, n]
+    out = np.zeros((rows, heads, dim), dtype=np.float32)
+    for h in range(heads):
+        kh = keys[:n, h // groups]  # [n, D]
+        vh = values[:n, h // groups]
+        scores = (q[:, h] @ kh.T).astype(np.float32) * scale  # [m, n]
+        scores = np.where(visible, scores, -np.inf)
+        scores = scores - scores.max(axis=-1, keepdims=True)
+        weights = np.exp(scores)
+        weights /= weights.sum(axis=-1, keepdims=True)
+        out[:, h] = weights @ vh
+    return out
+
+
 def kv_append(key_cache, value_cache, k, v, write_blocks, write_offsets, write_mask=None,
               active_rows=None):
     """In place: ``cache[block_r, offset_r] = k[r]`` for enabled rows.

@@ -55,7 +55,7 @@ int main(void) {
   int64_t wblocks[ROWS], woffs[ROWS];
   if (!hk || !hv || !hq || !knew || !vnew || !out || !out2) return fail("host allocation");
 
-  if (vrh_abi_version() != 4) return fail("vrh_abi_version() != 4");
+  if (vrh_abi_version() != 5) return fail("vrh_abi_version() != 5");
   for (size_t i = 0; i < pool_floats; ++i) {
     hk[i] = rnd();
     hv[i] = rnd();
@@ -113,7 +113,7 @@ int main(void) {
 
   /* 2. append (one layer view: block stride BS*slot, token stride slot). */
   if (vrh_kv_append(VRH_DTYPE_F32, dk, dv, BS * slot, slot, D, 0, dknew, dvnew, slot, D, 0, slot,
-                    D, 0, dwb, dwo, dmask, NULL, ROWS, 1, KVH, D, 0) != VRH_OK)
+                    D, 0, dwb, dwo, dmask, NULL, ROWS, 1, KVH, D, BLOCKS, BS, 0) != VRH_OK)
     return fail(vrh_last_error());
   for (int r = 0; r < ROWS; ++r) {
     if (!mask[r]) continue;

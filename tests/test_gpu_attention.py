@@ -169,6 +169,37 @@ def test_decode_uses_64bit_physical_offsets(gpu):
     del key, value
 
 
+def test_decode_more_rows_than_one_launch(gpu):
+    """70,000 rows (one head, head_dim 32) with mixed lengths: the launcher
+    splits the rows into launches of 65,472 (whole 64-row groups for the
+    in-kernel longest-first ranking); every row must equal its own one-row
+    decode (batch invariance) and a seeded subsample the oracle, including
+    rows on both sides of the launch boundary."""
+    from vllm_rlt.kernels.hip_attention import paged_attention
+
+    rows, block = 70000, 16
+    gen = torch.Generator().manual_seed(31)
+    lengths = torch.randint(0, 300, (rows,), generator=gen, dtype=torch.int32)
+    lengths[65470:65475] = torch.tensor([299, 0, 17, 160, 1], dtype=torch.int32)
+    width = 19
+    pool_blocks = 4096
+    k = torch.randn(pool_blocks, block, 1, 32, generator=gen).to(torch.bfloat16).to(gpu)
+    v = torch.randn(pool_blocks, block, 1, 32, generator=gen).to(torch.bfloat16).to(gpu)
+    tables = torch.randint(0, pool_blocks, (rows, width), generator=gen,
+                           dtype=torch.int32).to(gpu)
+    q = torch.randn(rows, 1, 32, generator=gen).to(torch.bfloat16).to(gpu)
+    context = lengths.to(gpu)
+    out = paged_attention(q, k, v, tables, context)
+    picks = sorted({0, 1, 65471, 65472, 65473, 65474, rows - 1,
+                    *torch.randint(0, rows, (40,), generator=gen).tolist()})
+    for r in picks:
+        single = paged_attention(q[r : r + 1], k, v, tables[r : r + 1], context[r : r + 1])
+        assert torch.equal(out[r : r + 1], single), r
+    idx = torch.tensor(picks, device=gpu)
+    want = oracle_decode(q[idx], k, v, tables[idx], context[idx])
+    assert_close(out[idx], want, torch.bfloat16)
+
+
 def test_decode_closed_forms(gpu):
     """Length 1 returns V exactly; constant keys return the mean of V."""
     from vllm_rlt.kernels.hip_attention import paged_attention

@@ -81,6 +81,38 @@ def test_append_many_rows_and_layers_in_one_launch(gpu):
     assert torch.equal(got_v.transpose(0, 1), v)
 
 
+def test_append_skips_out_of_range_addresses(gpu):
+    """A block id outside the pool or an offset outside the block writes
+    nothing (the reference's index_put would raise; here the pool is never
+    written outside its blocks), and every in-range row is still written,
+    through both the Python adapter and the torch operator."""
+    from vllm_rlt.kernels._extension import load_extension
+    from vllm_rlt.kernels.hip_attention import kv_append
+
+    load_extension()
+    for via_op in (False, True):
+        key_pool = pool((9, 2, 16, 4, 32), torch.bfloat16, gpu, 10)
+        value_pool = pool((9, 2, 16, 4, 32), torch.bfloat16, gpu, 11)
+        # a guard region after the pool: the layer view's last block is followed
+        # by other memory of the same allocation
+        kc, vc = key_pool[:8, 1], value_pool[:8, 1]
+        before_k, before_v = key_pool.clone(), value_pool.clone()
+        k = pool((5, 4, 32), torch.bfloat16, gpu, 12)
+        v = pool((5, 4, 32), torch.bfloat16, gpu, 13)
+        blocks = torch.tensor([0, 8, -1, 3, 7], dtype=torch.int64, device=gpu)
+        offsets = torch.tensor([1, 0, 2, 16, 15], dtype=torch.int64, device=gpu)
+        if via_op:
+            torch.ops.vllm_rlt_hip.kv_append(kc, vc, k, v, blocks, offsets, None, None)
+        else:
+            kv_append(kc, vc, k, v, blocks, offsets)
+        torch.cuda.synchronize()
+        want_k, want_v = before_k.clone(), before_v.clone()
+        for r in (0, 4):  # the two in-range rows
+            want_k[blocks[r], 1, offsets[r]] = k[r]
+            want_v[blocks[r], 1, offsets[r]] = v[r]
+        assert torch.equal(key_pool, want_k) and torch.equal(value_pool, want_v)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_gather_is_bit_exact(gpu, dtype):
     from vllm_rlt.kernels.hip_attention import kv_gather

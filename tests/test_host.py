@@ -108,7 +108,8 @@ def test_backend_reports_selection_and_capabilities(monkeypatch):
     assert backend.info["requested_backend"] == "auto"
     caps = backend_capabilities(backend)
     assert caps.packed_prefill and caps.cuda_graphs and caps.device_context_lengths
-    assert caps.sliding_window and not caps.packed_matches_decode
+    assert caps.sliding_window and caps.packed_matches_decode
+    assert backend.info["packed_matches_decode_max_seqlen_q"] == 8
 
 
 def test_missing_library_is_an_import_error(monkeypatch, tmp_path):
@@ -146,7 +147,7 @@ def test_library_rejects_bad_arguments_without_a_gpu():
                                 1, 1, 1, 1, 0, None, 0, None)
     assert code == 1 and b"workspace" in lib.vrh_last_error()
     code = lib.vrh_kv_append(9, 1, 1, 1, 1, 1, 0, 1, 1, 1, 1, 0, 1, 1, 0, 1, 1, None, None, 1, 1,
-                             1, 1, None)
+                             1, 1, 0, 0, None)
     assert code == 1 and b"dtype" in lib.vrh_last_error()
     code = lib.vrh_kv_finalize_token(1, 1, 0, (ctypes.c_int64 * 1)(0), 1, 0,
                                      (ctypes.c_int32 * 1)(0), 1, 64, 64, 64, 64, None)

@@ -142,6 +142,38 @@ def test_prefill_matches_causal_sdpa():
     np.testing.assert_allclose(out, expected.transpose(0, 1).numpy(), atol=2e-6, rtol=2e-5)
 
 
+@pytest.mark.parametrize("groups", [1, 4])
+def test_causal_block_matches_row_oracle_and_sdpa(groups):
+    """causal_block (whole query tiles at once) equals paged_attention on the
+    per-query rows, and SDPA with the causal mask; a wrong mask offset, head
+    mapping or scale fails one of them."""
+    rng = np.random.default_rng(21 + groups)
+    dim, block, kv_heads = 16, 4, 2
+    heads = kv_heads * groups
+    n, q_len = 37, 9
+    pages = -(-n // block)
+    kc = rng.standard_normal((pages + 3, block, kv_heads, dim)).astype(np.float32)
+    vc = rng.standard_normal((pages + 3, block, kv_heads, dim)).astype(np.float32)
+    table = rng.permutation(pages + 3)[:pages].astype(np.int32)
+    q = rng.standard_normal((q_len, heads, dim)).astype(np.float32)
+    keys = history(kc, table[None], [n])[0]
+    values = history(vc, table[None], [n])[0]
+    positions = n - q_len + np.arange(q_len)
+    got = ref.causal_block(q, keys, values, positions)
+    rows = ref.paged_prefill(q, kc, vc, table[None], np.array([n], np.int32),
+                             np.array([0, q_len]))
+    np.testing.assert_allclose(got, rows, atol=1e-6, rtol=1e-5)
+    kt = torch.from_numpy(np.repeat(keys, groups, axis=1)).transpose(0, 1)
+    vt = torch.from_numpy(np.repeat(values, groups, axis=1)).transpose(0, 1)
+    mask = torch.arange(n)[None, :] <= torch.from_numpy(positions)[:, None]
+    expected = F.scaled_dot_product_attention(torch.from_numpy(q).transpose(0, 1), kt, vt,
+                                              attn_mask=mask)
+    np.testing.assert_allclose(got, expected.transpose(0, 1).numpy(), atol=2e-6, rtol=2e-5)
+    # a query at position 0 sees one key: its output is that value row
+    first = ref.causal_block(q[:1], keys, values, [0])
+    np.testing.assert_allclose(first[0], np.repeat(values[0], groups, axis=0), atol=1e-6)
+
+
 def test_bf16_rounding_matches_torch():
     x = np.random.default_rng(4).standard_normal(10000).astype(np.float32) * 100
     x[:4] = [np.inf, -np.inf, 0.0, -0.0]

@@ -98,6 +98,40 @@ def test_noalloc_grouped_query_mfma_twice(gpu):
         assert torch.equal(got, want)
 
 
+def test_noalloc_captured_in_a_graph_replays_like_eager(gpu):
+    """The allocation-free entry point under HIP-graph capture: replayed three
+    times, with eager decode calls on other inputs and synchronisations in
+    between (they overwrite the shared scratch), every replay equals the
+    eager result of the captured inputs."""
+    from vllm_rlt.kernels._hip import library
+    from vllm_rlt.kernels.hip_attention import paged_attention, paged_attention_noalloc
+
+    lib = library()
+    # resolves the scratch address of this device before capture
+    assert lib.vrh_paged_decode_noalloc_max_bytes() == 96 << 20
+    print("noalloc: graph capture, 48 rows up to 3000 tokens, 3 replays", flush=True)
+    q, k, v, tables, lengths = _inputs(48, 3000, seed=8)
+    other = _inputs(20, 2000, seed=9)
+    want = paged_attention(q, k, v, tables, lengths)
+    out = torch.full_like(q, float("nan"))
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        paged_attention_noalloc(q, k, v, tables, lengths, out=out)  # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_attention_noalloc(q, k, v, tables, lengths, out=out)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        paged_attention_noalloc(*other)  # overwrites the scratch between replays
+        torch.cuda.synchronize()
+
+
 def test_noalloc_rejects_sizes_beyond_the_scratch(gpu):
     from vllm_rlt.kernels._hip import library
 

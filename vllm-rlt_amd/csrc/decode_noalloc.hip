@@ -5,9 +5,12 @@
 // grow a pool, tight serving loops, harnesses that forbid hipMalloc). The
 // kernels are the ones of vrh_paged_decode; only the partials' home differs.
 //
-// `scratch` is one array per GPU, held until the process ends. Its address is
-// looked up once per device (hipGetSymbolAddress with that device current) and
-// kept; host code never passes the array's name itself to a kernel (on the
+// `scratch` is one array per GPU: 96 MiB of device memory reserved on every
+// GPU where this library's code object is loaded, whether or not the entry
+// point is ever called, and held until the process ends. Its address is
+// looked up once per device (hipGetSymbolAddress with that device current, at
+// the first vrh_paged_decode_noalloc_max_bytes or vrh_paged_decode_noalloc
+// call on it) and kept; host code never passes the array's name itself to a kernel (on the
 // host that name is only a stand-in, not a device address). The partials need
 // no initialisation: every split the merge reads is written by the same call
 // first. Calls that overlap on one GPU (different streams, or graphs replayed
@@ -62,7 +65,14 @@ void* scratch_address(const char* who) {
 
 }  // namespace
 
-extern "C" size_t vrh_paged_decode_noalloc_max_bytes(void) { return kScratchBytes; }
+// Also looks up the current device's scratch address, so that a caller can do
+// that before capturing a graph (the lookup is a runtime call, not a stream
+// operation, and is done at most once per device). A failed lookup is
+// reported by the first vrh_paged_decode_noalloc call instead.
+extern "C" size_t vrh_paged_decode_noalloc_max_bytes(void) {
+  scratch_address("vrh_paged_decode_noalloc_max_bytes");
+  return kScratchBytes;
+}
 
 extern "C" int vrh_paged_decode_noalloc(
     int dtype, void* out, const void* q, const void* key_cache, const void* value_cache,

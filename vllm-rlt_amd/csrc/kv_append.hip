@@ -15,10 +15,6 @@
 // of the step) reads whole contexts from HBM.
 #include "common.h"
 
-#ifndef VRH_APPEND_NT_STORE
-#define VRH_APPEND_NT_STORE 1
-#endif
-
 namespace vrh {
 namespace {
 
@@ -36,6 +32,8 @@ struct AppendArgs {
   int64_t k_row, k_head, k_layer;
   int64_t v_row, v_head, v_layer;
   int64_t row_base;
+  int64_t num_blocks;     // > 0: rows whose block id is outside [0, num_blocks) are skipped
+  int32_t block_size;     // > 0: rows whose offset is outside [0, block_size) are skipped
   int32_t vecs_per_head;  // head bytes / VECB
   int32_t vec_shift;      // log2(vecs_per_head) or -1
   int32_t vecs_per_row;   // kv_heads * vecs_per_head
@@ -58,20 +56,20 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
     jj = j - h * a.vecs_per_head;
   }
   const int64_t lay = blockIdx.z;
+  const int64_t block = a.blocks[row], offset = a.offsets[row];
+  // Out-of-range addresses write nothing (the pool is never written outside
+  // its blocks); in range is the caller's contract, as in the reference.
+  if (a.num_blocks > 0 && (block < 0 || block >= a.num_blocks)) return;
+  if (a.block_size > 0 && (offset < 0 || offset >= a.block_size)) return;
   // Block ids are promoted to 64 bits before the multiply: pools exceed 2^31 B.
-  const int64_t dst = a.blocks[row] * a.c_block + a.offsets[row] * a.c_token + h * a.c_head +
+  const int64_t dst = block * a.c_block + offset * a.c_token + h * a.c_head +
                       lay * a.c_layer + (int64_t)jj * VECB;
   const raw_t kv = *reinterpret_cast<const raw_t*>(a.k + row * a.k_row + h * a.k_head +
                                                    lay * a.k_layer + (int64_t)jj * VECB);
   const raw_t vv = *reinterpret_cast<const raw_t*>(a.v + row * a.v_row + h * a.v_head +
                                                    lay * a.v_layer + (int64_t)jj * VECB);
-#if VRH_APPEND_NT_STORE
   __builtin_nontemporal_store(kv, reinterpret_cast<raw_t*>(a.kc + dst));
   __builtin_nontemporal_store(vv, reinterpret_cast<raw_t*>(a.vc + dst));
-#else
-  *reinterpret_cast<raw_t*>(a.kc + dst) = kv;
-  *reinterpret_cast<raw_t*>(a.vc + dst) = vv;
-#endif
 }
 
 }  // namespace
@@ -88,7 +86,8 @@ extern "C" int vrh_kv_append(int dtype, void* key_cache, void* value_cache,
                              int64_t v_layer_stride, const int64_t* write_blocks,
                              const int64_t* write_offsets, const uint8_t* write_mask,
                              const int32_t* active_rows, int64_t rows, int32_t layers,
-                             int32_t kv_heads, int32_t head_dim, vrh_stream_t stream) {
+                             int32_t kv_heads, int32_t head_dim, int64_t num_blocks,
+                             int32_t block_size, vrh_stream_t stream) {
   const int es = dtype_bytes(dtype);
   VRH_CHECK_ARG(es > 0, "vrh_kv_append: unknown dtype %d", dtype);
   VRH_CHECK_ARG(rows >= 0 && layers >= 1 && kv_heads >= 1 && head_dim >= 1,
@@ -118,6 +117,8 @@ extern "C" int vrh_kv_append(int dtype, void* key_cache, void* value_cache,
   a.v_head = v_head_stride * es;
   a.v_layer = v_layer_stride * es;
   a.row_base = 0;
+  a.num_blocks = num_blocks;
+  a.block_size = block_size;
   const int64_t head_bytes = (int64_t)head_dim * es;
   const int vb = pick_vb({head_bytes, a.c_block, a.c_token, a.c_head, a.c_layer, a.k_row,
                           a.k_head, a.k_layer, a.v_row, a.v_head, a.v_layer},

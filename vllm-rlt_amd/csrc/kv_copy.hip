@@ -18,9 +18,6 @@
 
 #include "common.h"
 
-#ifndef VRH_FINALIZE_NT_STORE
-#define VRH_FINALIZE_NT_STORE 1
-#endif
 
 namespace vrh {
 namespace {
@@ -101,13 +98,8 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinalizeArgs a) {
   raw_t* vd = reinterpret_cast<raw_t*>(a.vc + dst * a.block_stride + off);
   // Non-temporal stores: the deeper planes' slots are written once here and
   // read by later steps' attention, which streams whole contexts.
-#if VRH_FINALIZE_NT_STORE
   __builtin_nontemporal_store(ks[j], kd + j);
   __builtin_nontemporal_store(vs[j], vd + j);
-#else
-  kd[j] = ks[j];
-  vd[j] = vs[j];
-#endif
 }
 
 constexpr int kMaxTokenDst = 64;

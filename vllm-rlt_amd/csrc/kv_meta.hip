@@ -20,7 +20,7 @@ void vrh_set_error(const char* fmt, ...) {
 }
 
 extern "C" const char* vrh_last_error(void) { return g_last_error; }
-extern "C" int vrh_abi_version(void) { return 4; }
+extern "C" int vrh_abi_version(void) { return 5; }
 
 namespace vrh {
 namespace {

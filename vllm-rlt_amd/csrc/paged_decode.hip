@@ -39,53 +39,18 @@
 namespace vrh {
 namespace {
 
-// Tuning knobs (compile-time): wave loads per chunk (in flight per lane for
-// each of K and V), minimum split length, next-chunk prefetch, non-temporal
-// K/V loads.
-#ifndef VRH_DECODE_U
-#define VRH_DECODE_U 8
-#endif
-#ifndef VRH_SPLIT_TOKENS
-#define VRH_SPLIT_TOKENS 128
-#endif
-#ifndef VRH_DECODE_NT
-#define VRH_DECODE_NT 1
-#endif
-#ifndef VRH_DECODE_PREFETCH
-#define VRH_DECODE_PREFETCH 0
-#endif
-
-#ifndef VRH_DECODE_LPT
-#define VRH_DECODE_LPT 1
-#endif
-#ifndef VRH_DECODE_MAX_HPW
-#define VRH_DECODE_MAX_HPW 8  // grouped-query heads one wave may serve
-#endif
-#ifndef VRH_MAX_SPLITS
-#define VRH_MAX_SPLITS 16
-#endif
-constexpr int kMaxSplits = VRH_MAX_SPLITS;
-constexpr int kSplitTokens = VRH_SPLIT_TOKENS;  // minimum tokens per split (whole pages)
-#ifndef VRH_DECODE_LINE_SHARED
-#define VRH_DECODE_LINE_SHARED 1
-#endif
-#ifndef VRH_DECODE_SHARED_HINT
-#define VRH_DECODE_SHARED_HINT 1
-#endif
-#ifndef VRH_DECODE_DOT2
-#define VRH_DECODE_DOT2 1
-#endif
+// Wave loads per chunk (in flight per lane for each of K and V), minimum and
+// maximum split length, grouped-query heads one wave may serve.
+constexpr int kMaxSplits = 16;
+constexpr int kSplitTokens = 128;  // minimum tokens per split (whole pages)
+constexpr int kMaxHpw = 8;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 
-constexpr int kU = VRH_DECODE_U;                // wave loads per chunk (K and V each)
+constexpr int kU = 8;                // wave loads per chunk (K and V each)
 
 template <typename T, int VEC>
 __device__ __forceinline__ typename Vec<T, VEC>::raw_t load_kv(const T* p) {
-#if VRH_DECODE_NT
   return load_raw_stream<T, VEC>(p);
-#else
-  return load_raw<T, VEC>(p);
-#endif
 }
 
 struct DecodeArgs {
@@ -231,7 +196,7 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
   // bf16 with 8-element vectors: the q.k product runs on packed bf16 pairs
   // (v_dot2 with fp32 accumulation, products exact in fp32) against the
   // unscaled q; the scale is applied to the reduced score.
-  constexpr bool kDot2 = VRH_DECODE_DOT2 && std::is_same<T, bf16_t>::value && VEC == 8;
+  constexpr bool kDot2 = std::is_same<T, bf16_t>::value && VEC == 8;
   uint32_t qp2[HPW][VEC / 2];
   float qf[HPW][VEC];
 #pragma unroll
@@ -261,7 +226,6 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
   const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)kvh * a.k_head + lane_dim;
   const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)kvh * a.v_head + lane_dim;
   const int32_t* table = a.tables + trow * a.table_stride;
-#if VRH_DECODE_SHARED_HINT
   // Shared prefixes start at page 0: only rows whose first page is their
   // neighbour's compare further pages (two uniform loads otherwise).
   bool share_prev = false, share_next = false;
@@ -271,7 +235,6 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
     if (trow > 0) share_prev = table[-a.table_stride] == first;
     if (trow + 1 < table_rows) share_next = table[a.table_stride] == first;
   }
-#endif
 
   // The split loop is instantiated twice: with the per-page sharing test and,
   // for rows that share no first page with a neighbour (all of a batch of
@@ -301,7 +264,6 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
         const int s_tb = max(tb, seg * a.block_size);
         const int s_te = min(te, (seg + 64) * a.block_size);
         if (s_tb >= s_te) continue;
-#if VRH_DECODE_SHARED_HINT
         // Pages this row shares with a neighbouring row of the batch (the same
         // block at the same table index: parallel samples of one prompt, batches
         // grouped by prefix) are read with ordinary loads, so that the rows'
@@ -314,7 +276,6 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
           if (in_seg && share_next) shared |= table[seg + lane + a.table_stride] == tbl;
           shared_pages = a.line_shared ? ~0ull : __ballot(shared);
         }
-#endif
         // Branch-free loads: positions past the end re-read the last valid token
         // (masked out of the softmax), so a chunk is one straight run of loads.
         auto issue = [&](int p0, raw_t (&kr)[U], raw_t (&vr)[U], auto stream_c) {
@@ -343,7 +304,6 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
         // The chunk at p0 is read with ordinary loads when one of its pages is
         // shared with a neighbouring row (wave-uniform).
         auto load_chunk = [&](int p0, raw_t (&kr)[U], raw_t (&vr)[U]) {
-#if VRH_DECODE_SHARED_HINT
           if constexpr (kHint) {
             const int last = min(p0 + CH, s_te) - 1;
             int lo, hi;
@@ -360,16 +320,11 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
               return;
             }
           }
-#endif
           issue(p0, kr, vr, std::true_type{});
         };
         raw_t kr[U], vr[U];
         load_chunk(s_tb, kr, vr);
         for (int p0 = s_tb; p0 < s_te; p0 += CH) {
-#if VRH_DECODE_PREFETCH
-          raw_t kn[U], vn[U];
-          if (p0 + CH < s_te) load_chunk(p0 + CH, kn, vn);
-#endif
           float sc[HPW][U];
           float mx[HPW];
 #pragma unroll
@@ -421,15 +376,7 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
           }
 #pragma unroll
           for (int h = 0; h < HPW; ++h) m[h] = mx[h];
-#if VRH_DECODE_PREFETCH
-#pragma unroll
-          for (int u = 0; u < U; ++u) {
-            kr[u] = kn[u];
-            vr[u] = vn[u];
-          }
-#else
           if (p0 + CH < s_te) load_chunk(p0 + CH, kr, vr);
-#endif
         }
       }
 
@@ -465,12 +412,10 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
       }
     }
   };
-#if VRH_DECODE_SHARED_HINT
   if (share_prev || share_next || a.line_shared) {
     run(std::true_type{});
     return;
   }
-#endif
   run(std::false_type{});
 }
 
@@ -478,7 +423,6 @@ __device__ __forceinline__ void decode_work(const DecodeArgs& a, int64_t row, in
 // first split (rotated). False when the slot has no row.
 __device__ __forceinline__ bool grid_slot(const DecodeArgs& a, int64_t& row, int& split0) {
   row = a.row_base + blockIdx.z;
-#if VRH_DECODE_LPT
   // Longest splits first: within each group of 64 consecutive rows, grid
   // row slot z takes the row of rank z by split length (pages per split,
   // descending; ties keep row order, so rows whose splits are equally long,
@@ -499,10 +443,12 @@ __device__ __forceinline__ bool grid_slot(const DecodeArgs& a, int64_t& row, int
     const int slot = (int)(blockIdx.z & 63);
     // Rank only when the group's split lengths differ by 2x or more: only then
     // does the order shorten the drain (and rows of equal split length, such
-    // as rows sharing a prefix, keep their dispatch neighbourhood).
+    // as rows sharing a prefix, keep their dispatch neighbourhood). kmin is
+    // the smallest key of the group's rows (lanes past the last row are left
+    // out); a zero-length row makes it 0, so such a group is always ranked.
     const int kmax = wave_max_i(key);
     const int kmin = -wave_max_i(key >= 0 ? -key : INT32_MIN + 1);
-    if (kmax >= 2 * kmin || (kmin < 0 && kmax >= 0)) {
+    if (kmax >= 2 * kmin) {
       int rank = 0;
 #pragma unroll
       for (int j = 0; j < 64; ++j) {
@@ -514,7 +460,6 @@ __device__ __forceinline__ bool grid_slot(const DecodeArgs& a, int64_t& row, int
       row = g0 + __builtin_ffsll((long long)hit) - 1;
     }
   }
-#endif
   // Workgroup L = x + gx * (head + heads * row) runs on XCD L % 8. Rows need
   // different split counts, so with split = x the low split indices (present
   // in every row) would pile onto the same XCDs; rotating the split index by
@@ -550,12 +495,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
 //    A-operand with the same token slots.
 //  * Partition, split rotation, longest-first order and partials are those of
 //    the VALU kernel, so the same merge kernel combines the splits.
-#ifndef VRH_DECODE_MFMA_GQA
-#define VRH_DECODE_MFMA_GQA 1
-#endif
-#ifndef VRH_MFMA_ALL_GROUPS
-#define VRH_MFMA_ALL_GROUPS 8  // groups this large always take the MFMA kernel
-#endif
+constexpr int kMfmaAllGroups = 8;  // groups this large always take the MFMA kernel
 constexpr int kMfmaMinGroup = 3;    // smaller groups use the VALU kernel
 constexpr int kMfmaHeads = 16;      // q heads per tile (MFMA columns)
 constexpr int kMfmaChunk = 32;      // tokens per PV step
@@ -1017,7 +957,7 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.window = window;
   a.table_width = table_width;
-  a.line_shared = VRH_DECODE_SHARED_HINT && VRH_DECODE_LINE_SHARED && ((int64_t)head_dim * es) % 128 != 0;
+  a.line_shared = ((int64_t)head_dim * es) % 128 != 0;
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
   // Pages per split: at least kSplitTokens tokens; without a workspace every
   // row is a single split (pages can never exceed the table width).
@@ -1029,7 +969,7 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
   int hpw = 1;
   if (vec * es == 16 && lpt >= 4 && lpt <= 16)
     for (int h : {8, 4, 2})
-      if (a.group % h == 0 && h <= VRH_DECODE_MAX_HPW) {
+      if (a.group % h == 0 && h <= kMaxHpw) {
         hpw = h;
         break;
       }
@@ -1038,10 +978,9 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
   // or 3 to 7 heads that the VALU kernel cannot serve from one wave (it would
   // re-read K/V); groups of 2 and 4 stay on the VALU kernel, which is as fast
   // there (measured: 4 heads per wave 454 against 496 us at 256 rows).
-  const bool mfma_gqa = VRH_DECODE_MFMA_GQA &&
-                        (dtype == VRH_DTYPE_BF16 || dtype == VRH_DTYPE_F16) && vec * es == 16 &&
+  const bool mfma_gqa = (dtype == VRH_DTYPE_BF16 || dtype == VRH_DTYPE_F16) && vec * es == 16 &&
                         (head_dim == 64 || head_dim == 128) && a.group >= kMfmaMinGroup &&
-                        a.group <= kMfmaHeads && (a.group >= VRH_MFMA_ALL_GROUPS || hpw < a.group);
+                        a.group <= kMfmaHeads && (a.group >= kMfmaAllGroups || hpw < a.group);
   // Largest split count any row of this table width can need: the grid is a
   // function of shapes only (graph capture), never of device lengths.
   const int max_pages = std::max(1, table_width);

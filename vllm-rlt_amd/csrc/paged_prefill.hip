@@ -755,18 +755,32 @@ bool launch_prefill(int d, dim3 grid, hipStream_t s, const PrefillArgs& a) {
 using namespace vrh;
 
 // Sequences with at most this many queries (decode rows riding in a packed
-// batch) run through the split-KV decode kernel instead of 64-query MFMA tiles.
+// batch) run through the split-KV decode kernel instead of MFMA tiles.
 constexpr int kDecodeQ = 1;
+// A batch whose sequences all have at most kExactQ queries (max_seqlen_q <=
+// kExactQ: speculative verification, decode-only batches) runs every query as
+// a decode row, so each packed query reproduces single-query decode bit for
+// bit (the decode partition depends only on the row's own length).
+constexpr int kExactQ = 8;
+
+// Queries per sequence that the decode kernel handles (rows per sequence of
+// its expanded grid).
+static int decode_route_q(int32_t max_seqlen_q) {
+  return max_seqlen_q >= 1 && max_seqlen_q <= kExactQ ? max_seqlen_q : kDecodeQ;
+}
 
 // Workspace: split-KV partials of the decode rows, then the dispatch order
 // (int32 per sequence, 256-byte aligned).
-static size_t decode_part_bytes(int64_t num_seqs, int32_t q_heads, int32_t head_dim) {
-  return (vrh_paged_decode_workspace_bytes(num_seqs * kDecodeQ, q_heads, head_dim) + 255) / 256 * 256;
+static size_t decode_part_bytes(int64_t num_seqs, int32_t max_seqlen_q, int32_t q_heads,
+                                int32_t head_dim) {
+  const int64_t rows = num_seqs * decode_route_q(max_seqlen_q);
+  return (vrh_paged_decode_workspace_bytes(rows, q_heads, head_dim) + 255) / 256 * 256;
 }
 
-extern "C" size_t vrh_paged_prefill_workspace_bytes(int64_t num_seqs, int32_t q_heads,
-                                                    int32_t head_dim) {
-  return decode_part_bytes(num_seqs, q_heads, head_dim) + (size_t)num_seqs * sizeof(int32_t);
+extern "C" size_t vrh_paged_prefill_workspace_bytes(int64_t num_seqs, int32_t max_seqlen_q,
+                                                    int32_t q_heads, int32_t head_dim) {
+  return decode_part_bytes(num_seqs, max_seqlen_q, q_heads, head_dim) +
+         (size_t)num_seqs * sizeof(int32_t);
 }
 
 extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void* key_cache,
@@ -785,7 +799,7 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
                 "vrh_paged_prefill: bad sizes");
   VRH_CHECK_ARG(q_heads >= 1 && kv_heads >= 1 && q_heads % kv_heads == 0,
                 "vrh_paged_prefill: query heads must be a positive multiple of KV heads");
-  VRH_CHECK_ARG(num_seqs < (1ll << 31) / kDecodeQ, "vrh_paged_prefill: too many sequences");
+  VRH_CHECK_ARG(num_seqs < (1ll << 31) / kExactQ, "vrh_paged_prefill: too many sequences");
   if (num_seqs == 0 || total_q == 0) return VRH_OK;
   VRH_CHECK_ARG(out && q && key_cache && value_cache && block_tables && context_lengths &&
                     cu_seqlens_q,
@@ -798,19 +812,27 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
               k_head_stride % 8 == 0 && v_block_stride % 8 == 0 && v_token_stride % 8 == 0 &&
               v_head_stride % 8 == 0;
   for (const void* p : {(const void*)out, q, key_cache, value_cache}) mfma = mfma && ((uintptr_t)p % 16 == 0);
+  const bool route_decode =
+      workspace != nullptr &&
+      workspace_bytes >= vrh_paged_prefill_workspace_bytes(num_seqs, max_seqlen_q, q_heads, head_dim);
+  const int route_q = decode_route_q(max_seqlen_q);
   if (!mfma) {
+    // Every query is a decode row: with a workspace and max_seqlen_q <=
+    // kExactQ through the split-KV rows that single-query decode uses (bit
+    // for bit the same), otherwise one split per row.
+    const bool exact = route_decode && route_q == max_seqlen_q;
     return vrh_decode_rows(dtype, out, q, key_cache, value_cache, block_tables, context_lengths,
-                           cu_seqlens_q, (int32_t)num_seqs, 0, total_q, q_heads, kv_heads,
-                           head_dim, block_size, table_width, table_stride, q_token_stride,
-                           q_head_stride, out_token_stride, out_head_stride, k_block_stride,
-                           k_token_stride, k_head_stride, v_block_stride, v_token_stride,
-                           v_head_stride, 0, nullptr, 0, s, "vrh_paged_prefill");
+                           cu_seqlens_q, (int32_t)num_seqs, exact ? route_q : 0,
+                           exact ? num_seqs * route_q : total_q, q_heads, kv_heads, head_dim,
+                           block_size, table_width, table_stride, q_token_stride, q_head_stride,
+                           out_token_stride, out_head_stride, k_block_stride, k_token_stride,
+                           k_head_stride, v_block_stride, v_token_stride, v_head_stride, 0,
+                           exact ? workspace : nullptr,
+                           exact ? decode_part_bytes(num_seqs, max_seqlen_q, q_heads, head_dim) : 0,
+                           s, "vrh_paged_prefill");
   }
   VRH_CHECK_ARG(max_seqlen_q >= 1, "vrh_paged_prefill: max_seqlen_q must be positive");
   VRH_CHECK_ARG(q_heads <= 65535, "vrh_paged_prefill: too many heads");
-  const bool route_decode =
-      workspace != nullptr &&
-      workspace_bytes >= vrh_paged_prefill_workspace_bytes(num_seqs, q_heads, head_dim);
   PrefillArgs a;
   a.out = out;
   a.q = q;
@@ -834,7 +856,7 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   a.block_size = block_size;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.table_width = table_width;
-  a.skip_q = route_decode ? kDecodeQ : 0;
+  a.skip_q = route_decode ? route_q : 0;
   {
     // Rows one staging instruction covers: 64 lanes of 16 bytes over rows of
     // head_dim / 8 chunks; the fast addressing needs them on one page.
@@ -855,8 +877,8 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   // workspace); larger batches use the ordering kernel and the workspace.
   a.rank_in_kernel = VRH_PREFILL_RANK_IN_KERNEL && num_seqs > 1 && num_seqs <= 64;
   if (route_decode && num_seqs > 1 && num_seqs <= kOrderMax && !a.rank_in_kernel) {
-    int32_t* order = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
-                                                decode_part_bytes(num_seqs, q_heads, head_dim));
+    int32_t* order = reinterpret_cast<int32_t*>(
+        static_cast<char*>(workspace) + decode_part_bytes(num_seqs, max_seqlen_q, q_heads, head_dim));
     hipLaunchKernelGGL(prefill_order_kernel, dim3(1), dim3(1024), 0, s, cu_seqlens_q,
                        context_lengths, (int32_t)num_seqs, a.skip_q,
                        (int64_t)table_width * block_size, order);
@@ -865,19 +887,24 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   const int64_t groups = num_seqs * kv_heads;
   const int64_t launched = (groups + 7) / 8 * 8 * (int64_t)a.group * a.qblocks;
   VRH_CHECK_ARG(launched < (1ll << 31), "vrh_paged_prefill: too many work items");
-  const bool ok = dtype == VRH_DTYPE_BF16
-                      ? launch_prefill<bf16_t>(head_dim, dim3((unsigned)launched), s, a)
-                      : launch_prefill<f16_t>(head_dim, dim3((unsigned)launched), s, a);
-  VRH_CHECK_ARG(ok, "vrh_paged_prefill: no kernel for head_dim %d", head_dim);
+  // With every sequence routed to the decode kernel (max_seqlen_q <= the
+  // routed query count) the MFMA launch would have no work.
+  if (a.skip_q < max_seqlen_q) {
+    const bool ok = dtype == VRH_DTYPE_BF16
+                        ? launch_prefill<bf16_t>(head_dim, dim3((unsigned)launched), s, a)
+                        : launch_prefill<f16_t>(head_dim, dim3((unsigned)launched), s, a);
+    VRH_CHECK_ARG(ok, "vrh_paged_prefill: no kernel for head_dim %d", head_dim);
+  }
   if (route_decode) {
-    // Decode rows of the packed batch: split-KV single-query kernel.
+    // Short sequences of the packed batch: one split-KV decode row per query
+    // (row r is query r % route_q of sequence r / route_q).
     const int rc = vrh_decode_rows(
         dtype, out, q, key_cache, value_cache, block_tables, context_lengths, cu_seqlens_q,
-        (int32_t)num_seqs, kDecodeQ, num_seqs * kDecodeQ, q_heads, kv_heads, head_dim,
+        (int32_t)num_seqs, route_q, num_seqs * route_q, q_heads, kv_heads, head_dim,
         block_size, table_width, table_stride, q_token_stride, q_head_stride, out_token_stride,
         out_head_stride, k_block_stride, k_token_stride, k_head_stride, v_block_stride,
         v_token_stride, v_head_stride, 0, workspace,
-        decode_part_bytes(num_seqs, q_heads, head_dim), s, "vrh_paged_prefill");
+        decode_part_bytes(num_seqs, max_seqlen_q, q_heads, head_dim), s, "vrh_paged_prefill");
     if (rc != VRH_OK) return rc;
   }
   VRH_RETURN_LAUNCH("vrh_paged_prefill");

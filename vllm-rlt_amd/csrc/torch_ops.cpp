@@ -121,7 +121,7 @@ at::Tensor paged_prefill(const at::Tensor& q_in, const at::Tensor& kc, const at:
   at::Tensor out = at::empty_like(q);
   if (q.size(0) == 0 || seqs == 0) return out;
   const int32_t heads = (int32_t)q.size(1), dim = (int32_t)q.size(2);
-  const size_t nbytes = vrh_paged_prefill_workspace_bytes(seqs, heads, dim);
+  const size_t nbytes = vrh_paged_prefill_workspace_bytes(seqs, (int32_t)max_seqlen_q, heads, dim);
   at::Tensor workspace = at::empty({(int64_t)nbytes}, q.options().dtype(at::kByte));
   check_rc(vrh_paged_prefill(dtype_code(q), out.data_ptr(), q.data_ptr(), kc.data_ptr(),
                              vc.data_ptr(), tables.data_ptr<int32_t>(),
@@ -182,7 +182,8 @@ void kv_append(const at::Tensor& kc, const at::Tensor& vc, const at::Tensor& k,
                          mask.has_value() ? reinterpret_cast<const uint8_t*>(mask_c.data_ptr())
                                           : nullptr,
                          active.has_value() ? active->data_ptr<int32_t>() : nullptr, rows, 1,
-                         (int32_t)kc.size(2), (int32_t)kc.size(3), stream_of(kc)),
+                         (int32_t)kc.size(2), (int32_t)kc.size(3), kc.size(0),
+                         (int32_t)kc.size(1), stream_of(kc)),
            "vrh_kv_append");
 }
 

@@ -66,11 +66,19 @@ HIP_CAPABILITIES = BackendCapabilities(
     packed_prefill=True,
     cuda_graphs=True,
     async_scheduling=True,
-    # Packed bf16 prefill uses MFMA tiles; decode uses a split-KV VALU kernel.
-    packed_matches_decode=False,
+    # A packed call with max_seqlen_q <= PACKED_DECODE_EXACT_Q runs every query
+    # as a split-KV decode row (the partition depends only on the row's own
+    # length), so it reproduces single-query decode bit for bit; longer packed
+    # sequences use MFMA tiles.
+    packed_matches_decode=True,
     device_context_lengths=True,
     sliding_window=True,
 )
+
+# Largest max_seqlen_q for which packed rows equal single-query decode exactly
+# (speculative verification packs draft + 1 tokens per request,
+# worker/speculative.py:176-178).
+PACKED_DECODE_EXACT_Q = 8
 
 # Names the reference accepts; all but ``hip``/``auto`` belong to the reference.
 _REFERENCE_ONLY = ("torch", "triton", "flash_attn", "flash_attn_2", "flash_attn_3",
@@ -116,7 +124,8 @@ def _create_explicit(backend, device, dtype, head_dim, block_size) -> AttentionB
 
     library()
     return AttentionBackend(HipPagedAttention(), HIP_CAPABILITIES,
-                            {"backend": "hip", "arch": arch})
+                            {"backend": "hip", "arch": arch,
+                             "packed_matches_decode_max_seqlen_q": PACKED_DECODE_EXACT_Q})
 
 
 def create_backend(

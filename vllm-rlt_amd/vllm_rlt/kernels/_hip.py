@@ -19,7 +19,7 @@ from functools import cache
 LIBRARY_NAME = "libvllm_rlt_hip.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "_lib",
                             LIBRARY_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 VRH_DTYPE_F32, VRH_DTYPE_F16, VRH_DTYPE_BF16 = 0, 1, 2
 
@@ -36,7 +36,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "vrh_kv_append": (
         _INT,
         [_INT, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P,
-         _P, _P, _I64, _I32, _I32, _I32, _P],
+         _P, _P, _I64, _I32, _I32, _I32, _I64, _I32, _P],
     ),
     "vrh_paged_decode_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
     "vrh_paged_decode": (
@@ -55,7 +55,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
         [_INT, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _I64,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _SZ, _P],
     ),
-    "vrh_paged_prefill_workspace_bytes": (_SZ, [_I64, _I32, _I32]),
+    "vrh_paged_prefill_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
     "vrh_kv_gather": (_INT, [_P, _P, _P, _P, _P, _I64, _I32, _I64, _I64, _I64, _P]),
     "vrh_kv_finalize": (
         _INT, [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _P]

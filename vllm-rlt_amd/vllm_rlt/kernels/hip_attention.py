@@ -172,7 +172,8 @@ def paged_prefill_attention(q, key_cache, value_cache, block_tables, context_len
         return output
     cu_seqlens_q = cu_seqlens_q.contiguous()
     lib = library()
-    nbytes = lib.vrh_paged_prefill_workspace_bytes(sequences, q.shape[1], q.shape[2])
+    nbytes = lib.vrh_paged_prefill_workspace_bytes(sequences, int(max_seqlen_q), q.shape[1],
+                                                   q.shape[2])
     workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
     lib.check(
         lib.vrh_paged_prefill(
@@ -292,7 +293,7 @@ def _append(kc, vc, k, v, blocks, offsets, mask, active, *, layers, cache_layer_
             blocks.data_ptr(), offsets.data_ptr(),
             None if mask is None else mask.contiguous().data_ptr(),
             None if active is None else active.data_ptr(), rows, layers, kc.shape[2],
-            kc.shape[3], _stream(kc),
+            kc.shape[3], kc.shape[0], kc.shape[1], _stream(kc),
         ),
         "vrh_kv_append",
     )
