@@ -637,14 +637,17 @@ __device__ __forceinline__ void decode_work_mfma(const DecodeArgs& a, int64_t ro
       const int s_te = min(te, (seg + 64) * a.block_size);
       for (int p0 = s_tb; p0 < s_te; p0 += kMfmaChunk) {
         // Loads (branch-free: positions past the end re-read the last token).
+        // The A-operand layout gives each token 4 lanes (64 bytes) per
+        // instruction, so instructions c and c + 1 read the two halves of one
+        // 128-byte line: ordinary (L1-allocating) loads let the second half
+        // hit the line the first brought in.
         u32x4_t kop[2][DC];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int pos = min(p0 + 16 * t + col, s_te - 1);
           const T* kp = kbase + page_addr(pos, tbl, seg, a.k_block, a.k_token);
 #pragma unroll
-          for (int c = 0; c < DC; ++c)
-            kop[t][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kp + 32 * c));
+          for (int c = 0; c < DC; ++c) kop[t][c] = *reinterpret_cast<const u32x4_t*>(kp + 32 * c);
         }
         // V straight into the LDS tile. The previous chunk's transposed reads
         // have returned (its PV MFMAs consumed them), so the tile is free.

@@ -45,19 +45,12 @@ int vrh_decode_rows(int dtype, void* out, const void* q, const void* key_cache,
 namespace vrh {
 namespace {
 
-#ifndef VRH_PREFILL_WAVES
-#define VRH_PREFILL_WAVES 4
-#endif
-constexpr int kWaves = VRH_PREFILL_WAVES;  // waves per workgroup
+constexpr int kWaves = 4;                  // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kWQ = 32;                    // queries per wave
 constexpr int kBM = kWQ * kWaves;          // queries per workgroup
 constexpr int kSB = 32;                    // keys per sub-block (one pipeline step)
-#ifndef VRH_PREFILL_STAGES
-#define VRH_PREFILL_STAGES 4
-#endif
-constexpr int kStages = VRH_PREFILL_STAGES;  // LDS half-stages: one sub-block each
-static_assert(kStages >= 3 && kStages <= 4, "stages");
+constexpr int kStages = 4;                 // LDS stages: one sub-block each
 constexpr int kTableSeg = 512;             // page ids staged in LDS at a time
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
@@ -146,24 +139,15 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-#ifndef VRH_PREFILL_DMA
-#define VRH_PREFILL_DMA 1
-#endif
-
-#ifndef VRH_PREFILL_SAME_KV32
-#define VRH_PREFILL_SAME_KV32 1
-#endif
-#ifndef VRH_PREFILL_WG_PER_CU
-#define VRH_PREFILL_WG_PER_CU (VRH_PREFILL_WAVES == 8 ? 1 : 2)
-#endif
-// Two waves per SIMD: two 4-wave workgroups or one 8-wave workgroup per CU.
-constexpr int kWavesPerEu = VRH_PREFILL_WG_PER_CU * VRH_PREFILL_WAVES / 4;
+// Two workgroups per CU, two waves per SIMD.
+constexpr int kWgPerCu = 2;
+constexpr int kWavesPerEu = kWgPerCu * kWaves / 4;
 
 // Page addressing modes: kDiv (any block size), kShift (power of two).
 enum PageMode { kDiv = 0, kShift = 1 };
 
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(kThreads, VRH_PREFILL_WG_PER_CU)
+__global__ __launch_bounds__(kThreads, kWgPerCu)
 __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefill_kernel(PrefillArgs a) {
   constexpr int DC = D / 16;                   // 16-wide d chunks (QK^T k-steps)
   constexpr int DB = D / 32;                   // 32-row d blocks of O^T
@@ -284,8 +268,8 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
   };
   load_table(0);
 
-  // Sub-block `j` of K/V: global -> registers (gather), registers -> LDS
-  // stage (put). Store r of this wave fills slots 64 * (wave + 4r) .. + 63 of
+  // Sub-block `j` of K/V goes from the pages straight into an LDS stage.
+  // Staging instruction r of this wave fills slots 64 * (wave + 4r) .. + 63 of
   // the sub-block: slot v holds chunk (v % KCH) ^ swizzle(row) of key row
   // v / KCH. Branch-free: keys past `end` re-read key end - 1 (real data);
   // the softmax masks them.
@@ -307,10 +291,6 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
   const T* lane_v = vg + (int64_t)lane_row * a.v_token + lane_dof;
   const T* lane_k1 = kg + (int64_t)lane_in * a.k_token + lane_dof;
   const T* lane_v1 = vg + (int64_t)lane_in * a.v_token + lane_dof;
-  struct Regs { u32x4 k[NI]; u32x4 v[NI]; };
-#ifndef VRH_PREFILL_SADDR
-#define VRH_PREFILL_SADDR 1
-#endif
   // Byte offset of this lane's 16 bytes within one staging instruction's rows
   // (same for K and V when their strides match); 32-bit when it fits.
   const int64_t lane_koff64 = ((int64_t)lane_in * a.k_token + lane_dof) * (int64_t)sizeof(T);
@@ -370,14 +350,8 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
            (kPow2 ? lane_v : vg) + page * a.v_block + toks * a.v_token + dof);
     }
   };
-  auto gather = [&](int j, Regs& R) {
-    gather_to(j, [&](int r, const T* kp, const T* vp) {
-      R.k[r] = *reinterpret_cast<const u32x4*>(kp);
-      R.v[r] = *reinterpret_cast<const u32x4*>(vp);
-    });
-  };
   // Sub-block j straight into LDS stage `stage` (global_load_lds_dwordx4: lane
-  // l's 16 bytes land at M0 + 16 l, the same slots `put` writes). The loads
+  // l's 16 bytes land at M0 + 16 l, the slots described above). The loads
   // are issued as inline assembly so that the compiler neither waits for them
   // nor orders LDS reads behind them; the pipeline waits explicitly
   // (vm_wait below) before the barrier that publishes a stage.
@@ -385,7 +359,6 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
     constexpr int stage = decltype(stage_c)::value;
     const uint32_t kl = lds_offset(ks[stage]) + 1024 * wave;
     const uint32_t vl = lds_offset(vs[stage]) + 1024 * wave;
-#if VRH_PREFILL_SADDR
     const int k0 = j * kSB;
     if (kPow2 && a.uniform_pages && a.same_kv32 && lane_off32 && k0 + kSB <= end) {
       {
@@ -405,23 +378,11 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
       }
       return;
     }
-#endif
     gather_to(j, [&](int r, const T* kp, const T* vp) {
       lds_dma16(kp, __builtin_amdgcn_readfirstlane(kl + 1024 * kWaves * r));
       lds_dma16(vp, __builtin_amdgcn_readfirstlane(vl + 1024 * kWaves * r));
     });
   };
-  auto put = [&](auto stage_c, const Regs& R) {
-    constexpr int stage = decltype(stage_c)::value;
-#pragma unroll
-    for (int r = 0; r < NI; ++r) {
-      const int inst = wave + kWaves * r;
-      if (SB_INST % kWaves != 0 && inst >= SB_INST) continue;
-      *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(ks[stage]) + 1024 * inst + 16 * lane) = R.k[r];
-      *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(vs[stage]) + 1024 * inst + 16 * lane) = R.v[r];
-    }
-  };
-
   // Per-lane LDS byte offsets inside a half-stage (the swizzle depends on
   // row & 15, which the 16-key steps below leave unchanged):
   //  * K operand reads: row `col`, dims 16c + 8half;
@@ -545,15 +506,12 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
     else rescale(row_max(j, st, std::true_type{}));
   };
 
-  // Pipeline over 32-key sub-blocks, kStages (3 or 4) LDS stages, sub-block
-  // j in stage j % kStages. Step j:
+  // Pipeline over 32-key sub-blocks, four LDS stages, sub-block j in stage
+  // j % 4. Step j:
   //   barrier (sub-block j + 1 is in LDS and visible; every wave has
   //   finished step j - 1, the last reader of sub-block j - 1);
-  //   LDS-direct: load sub-block j + 3 into the stage of j - 1 (two steps of
-  //   latency to land). Register staging: store the registers holding
-  //   sub-block j + 2 into stage (j + 2) % kStages (which held sub-block
-  //   j - 1 or j - 2), then gather sub-block j + 3 into the same registers
-  //   (one step of latency);
+  //   load sub-block j + 3 straight into the stage of j - 1 (two steps of
+  //   latency to land);
   //   S1: every LDS operand read (K of j + 1, V of j), then the QK^T MFMAs of
   //       j + 1 interleaved with the probability VALU work of j;
   //   S2: PV of sub-block j (MFMA) interleaved with the mask / row max of
@@ -566,13 +524,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
   using H3 = std::integral_constant<int, 3>;
   f32x16 st = f32x16{};
   // LDS-direct staging: sub-block j + 3 loaded into LDS at step j (two steps
-  // of load latency). With it switched off, staging goes through registers
-  // (sub-block j + 3 gathered at step j, stored at step j + 1).
-#ifndef VRH_PREFILL_DMA_UNEVEN
-#define VRH_PREFILL_DMA_UNEVEN 1
-#endif
-  constexpr bool kDma = VRH_PREFILL_DMA && kStages == 4 &&
-                        (VRH_PREFILL_DMA_UNEVEN || SB_INST % kWaves == 0);
+  // of load latency).
   constexpr int kDmaPerStep = 2 * NI;  // K and V loads per wave per sub-block
   // Where the staging loads do not divide evenly (head dims 32 and 96), the
   // first SB_INST % kWaves waves issue NI loads of K and of V per sub-block
@@ -582,22 +534,14 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
     if (full_share) vm_wait<kDmaPerStep>();
     else vm_wait<2 * (NI - 1)>();
   };
-  Regs R;
   if (nsub > 0) {
-    if constexpr (kDma) {
-      dma(0, H0{});
-      if (nsub > 1) dma(1, H1{});
-      if (nsub > 2) {
-        dma(2, H2{});
-        dma_wait_newest();  // sub-blocks 0 and 1 have landed
-      } else {
-        vm_wait<0>();
-      }
+    dma(0, H0{});
+    if (nsub > 1) dma(1, H1{});
+    if (nsub > 2) {
+      dma(2, H2{});
+      dma_wait_newest();  // sub-blocks 0 and 1 have landed
     } else {
-      gather(0, R);
-      put(H0{}, R);
-      if (nsub > 1) { gather(1, R); put(H1{}, R); }
-      if (nsub > 2) gather(2, R);
+      vm_wait<0>();
     }
     __syncthreads();
     if (nsub_w > 0) {
@@ -609,21 +553,14 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
     auto step = [&](int j, auto hc) {
       constexpr int h = decltype(hc)::value;
       using Hn = std::integral_constant<int, (h + 1) % kStages>;
-      using Hp = std::integral_constant<int, (h + 2) % kStages>;
-      if constexpr (kDma) {
-        // Sub-block j + 1 (read by this step) must have landed; only the
-        // loads of j + 2 (issued one step ago) may still be in flight. The
-        // barrier then publishes it and frees the stage of j - 1 for j + 3.
-        using Hd = std::integral_constant<int, (h + 3) % kStages>;
-        if (j + 2 < nsub) dma_wait_newest();
-        else vm_wait<0>();
-        __syncthreads();
-        if (j + 3 < nsub) dma(j + 3, Hd{});
-      } else {
-        __syncthreads();
-        if (j + 2 < nsub) put(Hp{}, R);
-        if (j + 3 < nsub) gather(j + 3, R);
-      }
+      // Sub-block j + 1 (read by this step) must have landed; only the loads
+      // of j + 2 (issued one step ago) may still be in flight. The barrier
+      // then publishes it and frees the stage of j - 1 for j + 3.
+      using Hd = std::integral_constant<int, (h + 3) % kStages>;
+      if (j + 2 < nsub) dma_wait_newest();
+      else vm_wait<0>();
+      __syncthreads();
+      if (j + 3 < nsub) dma(j + 3, Hd{});
       if (j >= nsub_w) return;
       u32x4 pop[2];
       u32x4 vop[DB][2];
@@ -674,10 +611,8 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
       step(j + 1, H1{});
       if (j + 2 >= nsub) break;
       step(j + 2, H2{});
-      if constexpr (kStages > 3) {
-        if (j + 3 >= nsub) break;
-        step(j + 3, H3{});
-      }
+      if (j + 3 >= nsub) break;
+      step(j + 3, H3{});
     }
   }
   lsum += shfl_xor_f32(lsum, 32);
@@ -703,9 +638,6 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
 // j < i)}, so equal keys keep their order and the permutation is stable.
 // key = clamped length, or -1 for sequences the MFMA kernel skips.
 constexpr int kOrderMax = 2048;  // larger batches keep the identity order
-#ifndef VRH_PREFILL_RANK_IN_KERNEL
-#define VRH_PREFILL_RANK_IN_KERNEL 1
-#endif
 __global__ __launch_bounds__(1024) void prefill_order_kernel(const int32_t* cu, const int32_t* lengths,
                                                              int32_t num_seqs, int32_t skip_q,
                                                              int64_t cap, int32_t* order) {
@@ -864,7 +796,7 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
     const bool pow2_chunks = (chunks & (chunks - 1)) == 0;
     a.uniform_pages = pow2_chunks && a.bs_shift >= 0 && block_size % (64 / chunks) == 0;
   }
-  a.same_kv32 = VRH_PREFILL_SAME_KV32 && k_block_stride == v_block_stride &&
+  a.same_kv32 = k_block_stride == v_block_stride &&
                 k_token_stride == v_token_stride && k_block_stride >= 0 &&
                 k_block_stride < (1ll << 31) && k_token_stride >= 0 &&
                 k_token_stride < (1ll << 31);
@@ -875,7 +807,7 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   a.order = nullptr;
   // Up to 64 sequences are ranked inside the kernel (also without a
   // workspace); larger batches use the ordering kernel and the workspace.
-  a.rank_in_kernel = VRH_PREFILL_RANK_IN_KERNEL && num_seqs > 1 && num_seqs <= 64;
+  a.rank_in_kernel = num_seqs > 1 && num_seqs <= 64;
   if (route_decode && num_seqs > 1 && num_seqs <= kOrderMax && !a.rank_in_kernel) {
     int32_t* order = reinterpret_cast<int32_t*>(
         static_cast<char*>(workspace) + decode_part_bytes(num_seqs, max_seqlen_q, q_heads, head_dim));
