@@ -14,7 +14,9 @@ metadata as int32/int64 arrays. Caches are per-layer views
 Pinning (tests/test_oracle.py): attention against torch's
 ``scaled_dot_product_attention`` (an independent library routine), closed forms
 (length 0 -> zeros, length 1 -> V row, constant keys -> mean of V, the
-closed-form early-exit means of the reference's tests), window = slicing, the
+closed-form early-exit means of the reference's tests), window = slicing,
+:func:`causal_block` against the per-query rows of :func:`paged_attention`
+and against causal SDPA, the
 literal integer vectors of the reference's metadata tests, and brute-force
 loops for the integer kernels.
 """
