@@ -121,3 +121,23 @@ def test_backend_declares_the_bound(gpu):
     packed = backend.prefill(q, k, v, tables, context, cu, 8)
     rows, lens = serial_rows(tables, context, cu)
     assert torch.equal(packed, backend(q, k, v, rows, lens))
+
+
+def test_packed_rows_equal_decode_many_sequences(gpu):
+    """100 sequences of 1-8 queries (more than the 64 the prefill ranks in
+    its kernel): still every packed query equals its decode row."""
+    from vllm_rlt.kernels.hip_attention import paged_attention, paged_prefill_attention
+
+    gen = torch.Generator().manual_seed(77)
+    q_lens = torch.randint(1, 9, (100,), generator=gen).tolist()
+    q_lens[0] = 8
+    lengths = [max(q, n) for q, n in zip(q_lens, torch.randint(1, 3000, (100,),
+                                                                 generator=gen).tolist())]
+    print("packed==decode: 100 sequences", flush=True)
+    q, k, v, tables, context, cu = packed_batch(q_lens, lengths, 16, 16, 128, torch.bfloat16,
+                                                gpu, seed=78)
+    packed = paged_prefill_attention(q, k, v, tables, context, cu, 8)
+    rows, lens = serial_rows(tables, context, cu)
+    serial = paged_attention(q, k, v, rows, lens)
+    torch.cuda.synchronize()
+    assert torch.equal(packed, serial)

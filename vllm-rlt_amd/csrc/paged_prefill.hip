@@ -808,7 +808,10 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   // Up to 64 sequences are ranked inside the kernel (also without a
   // workspace); larger batches use the ordering kernel and the workspace.
   a.rank_in_kernel = num_seqs > 1 && num_seqs <= 64;
-  if (route_decode && num_seqs > 1 && num_seqs <= kOrderMax && !a.rank_in_kernel) {
+  // With every sequence routed to the decode kernel (max_seqlen_q <= the
+  // routed query count) the MFMA launch, and its ordering, would have no work.
+  const bool mfma_work = a.skip_q < max_seqlen_q;
+  if (mfma_work && route_decode && num_seqs > 1 && num_seqs <= kOrderMax && !a.rank_in_kernel) {
     int32_t* order = reinterpret_cast<int32_t*>(
         static_cast<char*>(workspace) + decode_part_bytes(num_seqs, max_seqlen_q, q_heads, head_dim));
     hipLaunchKernelGGL(prefill_order_kernel, dim3(1), dim3(1024), 0, s, cu_seqlens_q,
@@ -819,9 +822,7 @@ extern "C" int vrh_paged_prefill(int dtype, void* out, const void* q, const void
   const int64_t groups = num_seqs * kv_heads;
   const int64_t launched = (groups + 7) / 8 * 8 * (int64_t)a.group * a.qblocks;
   VRH_CHECK_ARG(launched < (1ll << 31), "vrh_paged_prefill: too many work items");
-  // With every sequence routed to the decode kernel (max_seqlen_q <= the
-  // routed query count) the MFMA launch would have no work.
-  if (a.skip_q < max_seqlen_q) {
+  if (mfma_work) {
     const bool ok = dtype == VRH_DTYPE_BF16
                         ? launch_prefill<bf16_t>(head_dim, dim3((unsigned)launched), s, a)
                         : launch_prefill<f16_t>(head_dim, dim3((unsigned)launched), s, a);
