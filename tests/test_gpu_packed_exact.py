@@ -141,3 +141,32 @@ def test_packed_rows_equal_decode_many_sequences(gpu):
     serial = paged_attention(q, k, v, rows, lens)
     torch.cuda.synchronize()
     assert torch.equal(packed, serial)
+
+
+def test_packed_exact_call_under_graph_capture(gpu):
+    """A verification-shaped packed call (max_seqlen_q <= 8) captured in a HIP
+    graph: every replay, with eager calls on other inputs in between, equals
+    the eager result bit for bit."""
+    from vllm_rlt.kernels.hip_attention import paged_prefill_attention
+
+    q_lens, lengths = CASES[1]
+    q, k, v, tables, context, cu = packed_batch(q_lens, lengths, 16, 16, 128, torch.bfloat16,
+                                                gpu, seed=90)
+    other = packed_batch(CASES[0][0], CASES[0][1], 16, 16, 128, torch.bfloat16, gpu, seed=91)
+    want = paged_prefill_attention(q, k, v, tables, context, cu, 8)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        paged_prefill_attention(q, k, v, tables, context, cu, 8)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = paged_prefill_attention(q, k, v, tables, context, cu, 8)
+    print("packed==decode: graph replays", flush=True)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        paged_prefill_attention(*other, 8)
+        torch.cuda.synchronize()
