@@ -140,6 +140,23 @@ def test_library_exports_every_declared_symbol():
     assert bound.vrh_paged_decode_workspace_bytes(64, 16, 128) >= 64 * 16 * 16 * 130 * 4
 
 
+def test_prefill_workspace_covers_the_decode_rows_it_routes():
+    """A packed batch with max_seqlen_q <= 8 runs every query as a decode row
+    (num_seqs x max_seqlen_q rows of split partials); longer batches route only
+    their one-query sequences (num_seqs rows). Both also hold the int32
+    dispatch order after 256-byte-aligned partials."""
+    lib = _hip.library()
+    dec = lib.vrh_paged_decode_workspace_bytes
+    pre = lib.vrh_paged_prefill_workspace_bytes
+    for seqs in (1, 7, 64, 100):
+        for max_q in (1, 2, 5, 8):
+            need = -(-dec(seqs * max_q, 16, 128) // 256) * 256
+            assert pre(seqs, max_q, 16, 128) == need + 4 * seqs
+        for max_q in (9, 512, 8192):
+            need = -(-dec(seqs, 16, 128) // 256) * 256
+            assert pre(seqs, max_q, 16, 128) == need + 4 * seqs
+
+
 def test_library_rejects_bad_arguments_without_a_gpu():
     lib = _hip.library()
     # rows > 0 with a null workspace fails validation before any launch
