@@ -8,11 +8,13 @@
 //
 // MFMA path (bf16/f16, head_dim a multiple of 32 up to 128):
 //  * Workgroup = 4 waves = 128 query rows of one (sequence, q head); each wave
-//    owns 32 queries. K/V arrive in 32-key sub-blocks staged into LDS (four
-//    stages, loaded straight into LDS three sub-blocks ahead) and shared by
+//    owns 32 queries. K/V arrive in 32-key sub-blocks staged into LDS (three
+//    stages, loaded straight into LDS two sub-blocks ahead) and shared by
 //    the 4 waves; one barrier per sub-block.
-//  * Each wave software-pipelines the sub-blocks: the QK^T MFMAs of sub-block
-//    j + 1 are interleaved with the softmax VALU work of sub-block j.
+//  * Three workgroups per CU (three waves per SIMD, at most 168 VGPRs): a
+//    wave runs QK^T, softmax and PV of one sub-block in order, reading each
+//    MFMA operand from LDS just before its MFMA, and the SIMD's other two
+//    waves fill the MFMA and VALU pipes while it waits.
 //  * S^T = K Q^T with v_mfma_f32_32x32x16_{bf16,f16}: A = K rows from LDS
 //    (16-byte reads), B = Q^T held in registers for the whole kernel.
 //    Output lane l holds query l % 32 and keys 8 * (j / 4) + 4 * (l / 32) + j % 4.
@@ -50,7 +52,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kWQ = 32;                    // queries per wave
 constexpr int kBM = kWQ * kWaves;          // queries per workgroup
 constexpr int kSB = 32;                    // keys per sub-block (one pipeline step)
-constexpr int kStages = 4;                 // LDS stages: one sub-block each
+constexpr int kStages = 3;                 // LDS stages: one sub-block each
 constexpr int kTableSeg = 512;             // page ids staged in LDS at a time
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
@@ -139,8 +141,8 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-// Two workgroups per CU, two waves per SIMD.
-constexpr int kWgPerCu = 2;
+// Three workgroups per CU, three waves per SIMD.
+constexpr int kWgPerCu = 3;
 constexpr int kWavesPerEu = kWgPerCu * kWaves / 4;
 
 // Page addressing modes: kDiv (any block size), kShift (power of two).
@@ -355,33 +357,52 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
   // are issued as inline assembly so that the compiler neither waits for them
   // nor orders LDS reads behind them; the pipeline waits explicitly
   // (vm_wait below) before the barrier that publishes a stage.
+  // Page ids are read for all of this wave's instructions before the first
+  // load is issued: the loads are `asm volatile` with a memory clobber, so a
+  // page-id read placed after one could not move ahead of it, and each
+  // instruction would wait for its own LDS round trip.
   auto dma = [&](int j, auto stage_c) {
     constexpr int stage = decltype(stage_c)::value;
     const uint32_t kl = lds_offset(ks[stage]) + 1024 * wave;
     const uint32_t vl = lds_offset(vs[stage]) + 1024 * wave;
     const int k0 = j * kSB;
+    auto skip = [&](int r) { return SB_INST % kWaves != 0 && wave + kWaves * r >= SB_INST; };
     if (kPow2 && a.uniform_pages && a.same_kv32 && lane_off32 && k0 + kSB <= end) {
       {
         const int last_page = page_of(k0 + kSB - 1);
         if (last_page >= tbl_base + kTableSeg) load_table(page_of(k0));
       }
+      uint64_t off[NI];
 #pragma unroll
       for (int r = 0; r < NI; ++r) {
-        const int inst = wave + kWaves * r;
-        if (SB_INST % kWaves != 0 && inst >= SB_INST) continue;  // no such instruction
-        const int pb = k0 + IR * inst;
-        const uint32_t page = __builtin_amdgcn_readfirstlane(tbl_lds[(pb >> a.bs_shift) - tbl_base]);
+        const int pb = k0 + IR * (wave + kWaves * r);
+        const uint32_t page = __builtin_amdgcn_readfirstlane(
+            tbl_lds[skip(r) ? 0 : (pb >> a.bs_shift) - tbl_base]);
         const uint32_t row_off = __builtin_amdgcn_readfirstlane(pb & (a.block_size - 1));
-        const uint64_t off = (uint64_t)page * (uint32_t)a.k_block + (uint64_t)row_off * (uint32_t)a.k_token;
-        lds_dma16_s(kg + off, lane_koff, __builtin_amdgcn_readfirstlane(kl + 1024 * kWaves * r));
-        lds_dma16_s(vg + off, lane_koff, __builtin_amdgcn_readfirstlane(vl + 1024 * kWaves * r));
+        off[r] = (uint64_t)page * (uint32_t)a.k_block + (uint64_t)row_off * (uint32_t)a.k_token;
+      }
+#pragma unroll
+      for (int r = 0; r < NI; ++r) {
+        if (skip(r)) continue;  // no such instruction
+        lds_dma16_s(kg + off[r], lane_koff, __builtin_amdgcn_readfirstlane(kl + 1024 * kWaves * r));
+        lds_dma16_s(vg + off[r], lane_koff, __builtin_amdgcn_readfirstlane(vl + 1024 * kWaves * r));
       }
       return;
     }
-    gather_to(j, [&](int r, const T* kp, const T* vp) {
-      lds_dma16(kp, __builtin_amdgcn_readfirstlane(kl + 1024 * kWaves * r));
-      lds_dma16(vp, __builtin_amdgcn_readfirstlane(vl + 1024 * kWaves * r));
+    const T* kp[NI];
+    const T* vp[NI];
+#pragma unroll
+    for (int r = 0; r < NI; ++r) kp[r] = vp[r] = nullptr;
+    gather_to(j, [&](int r, const T* k, const T* v) {
+      kp[r] = k;
+      vp[r] = v;
     });
+#pragma unroll
+    for (int r = 0; r < NI; ++r) {
+      if (skip(r)) continue;
+      lds_dma16(kp[r], __builtin_amdgcn_readfirstlane(kl + 1024 * kWaves * r));
+      lds_dma16(vp[r], __builtin_amdgcn_readfirstlane(vl + 1024 * kWaves * r));
+    }
   };
   // Per-lane LDS byte offsets inside a half-stage (the swizzle depends on
   // row & 15, which the 16-key steps below leave unchanged):
@@ -397,37 +418,6 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
 #pragma unroll
     for (int h = 0; h < 2; ++h) voff[db][h] = 2 * L::at(tr_row + 8 * h, 32 * db + tr_col);
 
-  // S^T = K Q^T for the sub-block in half-stage `stage`: element j holds key
-  // 8(j/4) + 4half + j%4 of the sub-block for query `col`.
-  auto kload = [&](auto stage_c, u32x4 (&kop)[DC]) {
-    constexpr int stage = decltype(stage_c)::value;
-    const char* kd = reinterpret_cast<const char*>(ks[stage]);
-#pragma unroll
-    for (int c = 0; c < DC; ++c) kop[c] = *reinterpret_cast<const u32x4*>(kd + koff[c]);
-  };
-  auto qk_mfma = [&](const u32x4 (&kop)[DC]) {
-    f32x16 st = f32x16{};
-#pragma unroll
-    for (int c = 0; c < DC; ++c) st = Mfma<T>::run(kop[c], qop[c], st);
-    return st;
-  };
-  // V^T A-operands of the sub-block in half-stage `stage`: lane l needs dim
-  // 32db + l % 32 at keys 16c + 4half + {0..3} and 16c + 8 + 4half + {0..3}
-  // (pop's k-slots): two transposed reads whose 16-lane group g covers dims
-  // 32db + 16(g & 1) .. +15 (lanes 4i + s address key i, dims +4s).
-  auto vload = [&](auto stage_c, u32x4 (&vop)[DB][2]) {
-    constexpr int stage = decltype(stage_c)::value;
-    const char* vd = reinterpret_cast<const char*>(vs[stage]);
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const char* vp = vd + 16 * c * D * 2;
-        const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][0]));
-        const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][1]));
-        vop[db][c] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      }
-  };
   // P^T B-operands of scores `st` (already masked, m current): per 16-key
   // chunk c, elements 8c .. 8c+7 of st, i.e. keys 16c + 4half + {0..3} and
   // 16c + 8 + 4half + {0..3}.
@@ -445,12 +435,6 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
 #pragma unroll
       for (int i = 0; i < 16; i += 2 * w) p[i] += p[i + w];
     lsum += p[0];
-  };
-  auto pv = [&](const u32x4 (&vop)[DB][2], const u32x4 (&pop)[2]) {
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) acc[db] = Mfma<T>::run(vop[db][c], pop[c], acc[db]);
   };
   // Causal / end mask of sub-block j (only where needed: the wave-uniform
   // test passes for sub-blocks entirely below this wave's first query and
@@ -506,25 +490,22 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
     else rescale(row_max(j, st, std::true_type{}));
   };
 
-  // Pipeline over 32-key sub-blocks, four LDS stages, sub-block j in stage
-  // j % 4. Step j:
-  //   barrier (sub-block j + 1 is in LDS and visible; every wave has
-  //   finished step j - 1, the last reader of sub-block j - 1);
-  //   load sub-block j + 3 straight into the stage of j - 1 (two steps of
-  //   latency to land);
-  //   S1: every LDS operand read (K of j + 1, V of j), then the QK^T MFMAs of
-  //       j + 1 interleaved with the probability VALU work of j;
-  //   S2: PV of sub-block j (MFMA) interleaved with the mask / row max of
-  //       j + 1 (VALU), then the lane-pair max and rescale.
+  // Pipeline over 32-key sub-blocks, three LDS stages, sub-block j in stage
+  // j % 3. Step j:
+  //   wait until sub-block j has landed (only the loads of j + 1, issued one
+  //   step ago, may still be in flight); barrier (sub-block j is visible to
+  //   every wave; every wave has finished step j - 1, the last reader of the
+  //   stage of j - 1);
+  //   load sub-block j + 2 straight into that stage (two steps of latency);
+  //   S^T = K Q^T of sub-block j, its mask, row max and lazy rescale, the
+  //   probabilities, then O^T += V^T P^T. Each K and V^T operand is read from
+  //   LDS right before its MFMA, which keeps the wave within the register
+  //   budget of three waves per SIMD.
   // The loop is unrolled by kStages so every stage address is a
   // compile-time offset.
   using H0 = std::integral_constant<int, 0>;
   using H1 = std::integral_constant<int, 1>;
   using H2 = std::integral_constant<int, 2>;
-  using H3 = std::integral_constant<int, 3>;
-  f32x16 st = f32x16{};
-  // LDS-direct staging: sub-block j + 3 loaded into LDS at step j (two steps
-  // of load latency).
   constexpr int kDmaPerStep = 2 * NI;  // K and V loads per wave per sub-block
   // Where the staging loads do not divide evenly (head dims 32 and 96), the
   // first SB_INST % kWaves waves issue NI loads of K and of V per sub-block
@@ -537,73 +518,36 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
   if (nsub > 0) {
     dma(0, H0{});
     if (nsub > 1) dma(1, H1{});
-    if (nsub > 2) {
-      dma(2, H2{});
-      dma_wait_newest();  // sub-blocks 0 and 1 have landed
-    } else {
-      vm_wait<0>();
-    }
-    __syncthreads();
-    if (nsub_w > 0) {
-      u32x4 kop[DC];
-      kload(H0{}, kop);
-      st = qk_mfma(kop);
-      mask_max(0, st);
-    }
     auto step = [&](int j, auto hc) {
       constexpr int h = decltype(hc)::value;
-      using Hn = std::integral_constant<int, (h + 1) % kStages>;
-      // Sub-block j + 1 (read by this step) must have landed; only the loads
-      // of j + 2 (issued one step ago) may still be in flight. The barrier
-      // then publishes it and frees the stage of j - 1 for j + 3.
-      using Hd = std::integral_constant<int, (h + 3) % kStages>;
-      if (j + 2 < nsub) dma_wait_newest();
+      using Hd = std::integral_constant<int, (h + 2) % kStages>;
+      if (j + 1 < nsub) dma_wait_newest();
       else vm_wait<0>();
       __syncthreads();
-      if (j + 3 < nsub) dma(j + 3, Hd{});
+      if (j + 2 < nsub) dma(j + 2, Hd{});
       if (j >= nsub_w) return;
+      const char* kd = reinterpret_cast<const char*>(ks[h]);
+      f32x16 st = f32x16{};
+#pragma unroll
+      for (int c = 0; c < DC; ++c)
+        st = Mfma<T>::run(*reinterpret_cast<const u32x4*>(kd + koff[c]), qop[c], st);
+      mask_max(j, st);
       u32x4 pop[2];
-      u32x4 vop[DB][2];
-      if (j + 1 < nsub_w) {
-        u32x4 kop[DC];
-        kload(Hn{}, kop);
-        vload(hc, vop);
-        __builtin_amdgcn_sched_barrier(0);
-        const f32x16 st_n = qk_mfma(kop);
-        probs(st, pop);
+      probs(st, pop);
+      // V^T A-operands: lane l needs dim 32db + l % 32 at keys 16c + 4half +
+      // {0..3} and 16c + 8 + 4half + {0..3} (pop's k-slots): two transposed
+      // reads whose 16-lane group g covers dims 32db + 16(g & 1) .. +15
+      // (lanes 4i + s address key i, dims +4s).
+      const char* vd = reinterpret_cast<const char*>(vs[h]);
 #pragma unroll
-        for (int i = 0; i < DC; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const char* vp = vd + 16 * c * D * 2;
+          const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][0]));
+          const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][1]));
+          acc[db] = Mfma<T>::run(u32x4{lo[0], lo[1], hi[0], hi[1]}, pop[c], acc[db]);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        // PV of sub-block j with the row max of j + 1 interleaved.
-        float mx;
-        st = st_n;
-        if (unmasked(j + 1)) {
-          pv(vop, pop);
-          mx = row_max(j + 1, st, std::false_type{});
-#pragma unroll
-          for (int i = 0; i < 2 * DB; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-          }
-        } else {
-          pv(vop, pop);
-          mx = row_max(j + 1, st, std::true_type{});
-#pragma unroll
-          for (int i = 0; i < 2 * DB; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        rescale(mx);
-      } else {
-        probs(st, pop);
-        vload(hc, vop);
-        pv(vop, pop);
-      }
     };
     for (int j = 0; j < nsub; j += kStages) {
       step(j, H0{});
@@ -611,8 +555,6 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
       step(j + 1, H1{});
       if (j + 2 >= nsub) break;
       step(j + 2, H2{});
-      if (j + 3 >= nsub) break;
-      step(j + 3, H3{});
     }
   }
   lsum += shfl_xor_f32(lsum, 32);
