@@ -13,8 +13,8 @@
 //    the 4 waves; one barrier per sub-block.
 //  * Three workgroups per CU (three waves per SIMD, at most 168 VGPRs): a
 //    wave runs QK^T, softmax and PV of one sub-block in order, reading each
-//    MFMA operand from LDS just before its MFMA, and the SIMD's other two
-//    waves fill the MFMA and VALU pipes while it waits.
+//    MFMA operand from LDS one MFMA ahead of its use, and the SIMD's other
+//    two waves fill the MFMA and VALU pipes while it waits.
 //  * S^T = K Q^T with v_mfma_f32_32x32x16_{bf16,f16}: A = K rows from LDS
 //    (16-byte reads), B = Q^T held in registers for the whole kernel.
 //    Output lane l holds query l % 32 and keys 8 * (j / 4) + 4 * (l / 32) + j % 4.
@@ -410,6 +410,11 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
   //  * transposed V reads: rows 4half + (lane & 15) / 4 (+ 8), dims 32db + tr_col.
   const int tr_row = 4 * half + ((lane & 15) >> 2);
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  // For 256-byte rows (D = 128) the swizzle gives these offsets in closed
+  // form, a per-lane base plus an XOR term of the compile-time index:
+  //   K chunk c:   kb0 + ((c ^ kt) << 5),
+  //   V block db:  vb[h] + ((db ^ vt) << 6)   (row + 8h flips only swizzle bits 0-1),
+  // which keeps 5 VGPRs live instead of 16; other head dims keep a table.
   uint32_t koff[DC], voff[DB][2];
 #pragma unroll
   for (int c = 0; c < DC; ++c) koff[c] = 2 * L::at(col, 16 * c + 8 * half);
@@ -417,6 +422,20 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int h = 0; h < 2; ++h) voff[db][h] = 2 * L::at(tr_row + 8 * h, 32 * db + tr_col);
+  const uint32_t kb0 = col * 256 + ((half ^ (L::swizzle(col) & 1)) << 4);
+  const uint32_t kt = L::swizzle(col) >> 1;
+  const uint32_t vb0 = tr_row * 256 + (((tr_col >> 3) ^ (L::swizzle(tr_row) & 3)) << 4) + (tr_col & 7) * 2;
+  const uint32_t vb1 =
+      (tr_row + 8) * 256 + (((tr_col >> 3) ^ (L::swizzle(tr_row + 8) & 3)) << 4) + (tr_col & 7) * 2;
+  const uint32_t vt = L::swizzle(tr_row) >> 2;
+  auto k_offset = [&](int c) -> uint32_t {
+    if constexpr (KCH == 16) return kb0 + ((c ^ kt) << 5);
+    else return koff[c];
+  };
+  auto v_offset = [&](int db, int h) -> uint32_t {
+    if constexpr (KCH == 16) return (h ? vb1 : vb0) + ((db ^ vt) << 6);
+    else return voff[db][h];
+  };
 
   // P^T B-operands of scores `st` (already masked, m current): per 16-key
   // chunk c, elements 8c .. 8c+7 of st, i.e. keys 16c + 4half + {0..3} and
@@ -499,8 +518,8 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
   //   load sub-block j + 2 straight into that stage (two steps of latency);
   //   S^T = K Q^T of sub-block j, its mask, row max and lazy rescale, the
   //   probabilities, then O^T += V^T P^T. Each K and V^T operand is read from
-  //   LDS right before its MFMA, which keeps the wave within the register
-  //   budget of three waves per SIMD.
+  //   LDS one MFMA ahead of its use (two operands live at most), which keeps
+  //   the wave within the register budget of three waves per SIMD.
   // The loop is unrolled by kStages so every stage address is a
   // compile-time offset.
   using H0 = std::integral_constant<int, 0>;
@@ -528,9 +547,17 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
       if (j >= nsub_w) return;
       const char* kd = reinterpret_cast<const char*>(ks[h]);
       f32x16 st = f32x16{};
+      // Each operand is read one MFMA ahead of its use, so a read's latency
+      // overlaps the MFMA before it (two in flight per wave at most, which
+      // the register budget of three waves per SIMD allows).
+      auto kread = [&](int c) { return *reinterpret_cast<const u32x4*>(kd + k_offset(c)); };
+      u32x4 kop[DC];
+      kop[0] = kread(0);
 #pragma unroll
-      for (int c = 0; c < DC; ++c)
-        st = Mfma<T>::run(*reinterpret_cast<const u32x4*>(kd + koff[c]), qop[c], st);
+      for (int c = 0; c < DC; ++c) {
+        if (c + 1 < DC) kop[c + 1] = kread(c + 1);
+        st = Mfma<T>::run(kop[c], qop[c], st);
+      }
       mask_max(j, st);
       u32x4 pop[2];
       probs(st, pop);
@@ -538,16 +565,27 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
       // {0..3} and 16c + 8 + 4half + {0..3} (pop's k-slots): two transposed
       // reads whose 16-lane group g covers dims 32db + 16(g & 1) .. +15
       // (lanes 4i + s address key i, dims +4s).
+      // V^T A-operands: lane l needs dim 32db + l % 32 at keys 16c + 4half +
+      // {0..3} and 16c + 8 + 4half + {0..3} (pop's k-slots): two transposed
+      // reads whose 16-lane group g covers dims 32db + 16(g & 1) .. +15
+      // (lanes 4i + s address key i, dims +4s).
+      // MFMA i takes c = i / DB, db = i % DB: consecutive MFMAs accumulate
+      // into different d blocks (each block still adds c = 0 before c = 1).
       const char* vd = reinterpret_cast<const char*>(vs[h]);
+      auto vread = [&](int i) {
+        const int c = i / DB, db = i % DB;
+        const char* vp = vd + 16 * c * D * 2;
+        const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + v_offset(db, 0)));
+        const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + v_offset(db, 1)));
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+      u32x4 vop[2 * DB];
+      vop[0] = vread(0);
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const char* vp = vd + 16 * c * D * 2;
-          const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][0]));
-          const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(vp + voff[db][1]));
-          acc[db] = Mfma<T>::run(u32x4{lo[0], lo[1], hi[0], hi[1]}, pop[c], acc[db]);
-        }
+      for (int i = 0; i < 2 * DB; ++i) {
+        if (i + 1 < 2 * DB) vop[i + 1] = vread(i + 1);
+        acc[i % DB] = Mfma<T>::run(vop[i], pop[i / DB], acc[i % DB]);
+      }
     };
     for (int j = 0; j < nsub; j += kStages) {
       step(j, H0{});
