@@ -565,10 +565,6 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEu, kWavesPerEu))) void paged_prefil
       // {0..3} and 16c + 8 + 4half + {0..3} (pop's k-slots): two transposed
       // reads whose 16-lane group g covers dims 32db + 16(g & 1) .. +15
       // (lanes 4i + s address key i, dims +4s).
-      // V^T A-operands: lane l needs dim 32db + l % 32 at keys 16c + 4half +
-      // {0..3} and 16c + 8 + 4half + {0..3} (pop's k-slots): two transposed
-      // reads whose 16-lane group g covers dims 32db + 16(g & 1) .. +15
-      // (lanes 4i + s address key i, dims +4s).
       // MFMA i takes c = i / DB, db = i % DB: consecutive MFMAs accumulate
       // into different d blocks (each block still adds c = 0 before c = 1).
       const char* vd = reinterpret_cast<const char*>(vs[h]);
